@@ -1,0 +1,128 @@
+"""ctypes binding of the gfx950 C-ABI library ``libpcp_attention_hip.so``.
+
+The library is built in-tree (``aws_training_study_amd/_lib``) by
+``aws_training_study_amd.build_native.build()``.  Nothing here falls back to
+another implementation: a missing or stale library raises ``RuntimeError``.
+The C declarations live in ``include/pcp_attention_hip.h``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_DIR = Path(__file__).resolve().parent / "_lib"
+LIB_NAME = "libpcp_attention_hip.so"
+
+ABI_VERSION = 1
+
+PCPA_OK = 0
+STATUS_NAMES = {
+    0: "PCPA_OK",
+    -1: "PCPA_ERR_NULL_POINTER",
+    -2: "PCPA_ERR_ABI_VERSION",
+    -3: "PCPA_ERR_BAD_SHAPE",
+    -4: "PCPA_ERR_BAD_DTYPE",
+    -5: "PCPA_ERR_UNSUPPORTED",
+    -6: "PCPA_ERR_MISALIGNED",
+    -7: "PCPA_ERR_LAUNCH",
+    -8: "PCPA_ERR_TOO_LARGE",
+    -9: "PCPA_ERR_BAD_SCALE",
+}
+
+DTYPE_BF16 = 1
+DTYPE_FP8_E4M3FN = 2
+
+FLAG_BF16_MFMA = 1
+
+# Every symbol the header declares; the CPU test suite checks they resolve.
+EXPORTED_SYMBOLS = (
+    "pcpa_abi_version",
+    "pcpa_status_string",
+    "pcpa_check_params",
+    "pcpa_history_attention",
+)
+
+
+class PcpaParams(ctypes.Structure):
+    """Mirror of ``pcpa_params`` (include/pcp_attention_hip.h)."""
+
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("pcp_size", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("local_q_len", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+        ("max_local_blocks", ctypes.c_int32),
+        ("num_pages", ctypes.c_int32),
+        ("q_dtype", ctypes.c_int32),
+        ("kv_dtype", ctypes.c_int32),
+        ("out_dtype", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float),
+        ("k_scale", ctypes.c_float),
+        ("v_scale", ctypes.c_float),
+        ("flags", ctypes.c_uint32),
+    ]
+
+
+class PcpaError(RuntimeError):
+    """A non-zero status returned by the C ABI."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+
+
+_lib: ctypes.CDLL | None = None
+
+
+def library_path() -> Path:
+    return LIB_DIR / LIB_NAME
+
+
+def load_library() -> ctypes.CDLL:
+    """Load the in-tree library once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = library_path()
+    if not path.exists():
+        raise RuntimeError(
+            f"HIP extension {path} is missing; build it with "
+            "`python -c 'import __graft_entry__ as g; g.build()'` "
+            "(or aws_training_study_amd.build_native.build())"
+        )
+    lib = ctypes.CDLL(os.fspath(path))
+    lib.pcpa_abi_version.restype = ctypes.c_int32
+    lib.pcpa_abi_version.argtypes = []
+    lib.pcpa_status_string.restype = ctypes.c_char_p
+    lib.pcpa_status_string.argtypes = [ctypes.c_int32]
+    lib.pcpa_check_params.restype = ctypes.c_int32
+    lib.pcpa_check_params.argtypes = [ctypes.POINTER(PcpaParams)]
+    lib.pcpa_history_attention.restype = ctypes.c_int32
+    lib.pcpa_history_attention.argtypes = [
+        ctypes.POINTER(PcpaParams),
+        ctypes.c_void_p,
+        ctypes.c_void_p,
+        ctypes.c_void_p,
+        ctypes.c_void_p,
+        ctypes.c_void_p,
+        ctypes.c_void_p,
+    ]
+    version = lib.pcpa_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}; rebuild it")
+    _lib = lib
+    return lib
+
+
+def status_string(status: int) -> str:
+    return load_library().pcpa_status_string(status).decode()
+
+
+def check(status: int) -> None:
+    if status != PCPA_OK:
+        raise PcpaError(status, status_string(status))

@@ -1,0 +1,524 @@
+// History-only PCP attention for MI355X (gfx950): kernels and C ABI.
+//
+// One launch computes, for every logical PCP rank, the attention of that
+// rank's current-token Q over the whole paged history (all ranks' cache
+// blocks), which the Trainium2 proof of concept computed with a device ring
+// (pcp_attention/kernel.py:84-554).  The ring order only changes the order of
+// online-softmax updates; here every query row walks the block table in
+// table order.
+//
+// Work decomposition
+//   * A "row" is one (Q head, current token) pair.  Rows that share a KV head
+//     (GQA group) are independent and are tiled 128 to a workgroup:
+//     4 waves x 32 rows.  Grid = (ceil(rows_per_kv_head / 128), num_kv_heads).
+//   * Keys are consumed in 64-key tiles staged through LDS (K tile and V tile,
+//     row-major [key][d], 16-byte chunks XOR-swizzled per key so that both the
+//     score-operand reads and the transposing V reads are bank-conflict free).
+//   * Scores are computed transposed, S^T = K . Q^T, with 32x32 MFMA tiles:
+//     K (from LDS) is the A operand, the wave's 32 Q rows are a register-
+//     resident B operand.  The accumulator of S^T holds, per lane, 16 keys of
+//     one query, which is exactly the B-operand layout of P^T in
+//     O^T += V^T . P^T once the K rows are permuted (key_of_row below).  So P
+//     goes from the score accumulator to the PV MFMA without leaving the lane,
+//     and V^T is read from the row-major V tile with ds_read_b64_tr_b8/b16.
+//   * FP8 KV: both GEMMs run as v_mfma_f32_32x32x64_f8f6f4 (e4m3 x e4m3).  Q
+//     is quantised to e4m3 per row (scale amax/448) when loaded; P is
+//     quantised to e4m3 after exp2.  BF16 KV: v_mfma_f32_32x32x16_bf16.
+//   * Online softmax in FP32 registers in the log2 domain: the per-row factor
+//     softmax_scale * k_scale * log2(e) (times the Q row scale) is applied in
+//     the exp2 argument.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "pcp_attention_hip.h"
+
+namespace pcpa {
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+#define PCPA_LDS(T, p) ((__attribute__((address_space(3))) T*)(p))
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRowsPerWave = 32;
+constexpr int kRowsPerGroup = kWaves * kRowsPerWave;
+constexpr int kKeyTile = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kFp8Max = 448.0f;
+// FP8 probabilities are computed as 2^(x - m + kPBiasLog2): the largest is 64,
+// and values down to 2^-12 of the row max stay in e4m3's normal range.  The
+// factor cancels in O / l because l sums the same biased values.
+constexpr float kPBiasLog2 = 6.0f;
+
+struct FwdArgs {
+    const uint8_t* q;
+    const uint8_t* kv;
+    const int32_t* block_table;
+    const int32_t* page_valid_len;
+    uint8_t* out;
+    int64_t page_stride;   // bytes of one page (K and V of every KV head)
+    int64_t head_stride;   // bytes of one head's K (or V) block
+    int32_t rows_per_head; // pcp * group * local_q
+    int32_t group_rows;    // group * local_q
+    int32_t local_q;
+    int32_t num_q_heads;
+    int32_t group;
+    int32_t num_kv_heads;
+    int32_t num_entries;   // pcp * max_local_blocks
+    int32_t num_pages;
+    int32_t block_size;
+    float score_scale;     // softmax_scale * k_scale * log2(e)
+    float v_scale;
+};
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+    return __uint_as_float(bits16 << 16);
+}
+
+// Max / sum of a value over lanes l and l^32 (the two k-groups of a 32x32
+// MFMA tile, which hold different keys of the same query).
+__device__ __forceinline__ float halves_max(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Key (within the 64-key tile) held by accumulator register r of score tile t
+// in lane half h.  The 32x32 accumulator puts row 8*(r/4) + 4*h + r%4 in
+// register r; K rows are ordered so that P^T comes out in PV B-operand order:
+//   FP8 (one PV MFMA eats 64 keys, 32 per lane half): key = 32h + 16t + r
+//   BF16 (one PV MFMA eats 16 keys, 8 per lane half):
+//        key = 32t + 16*(r/8) + 8h + r%8
+template <bool FP8>
+__device__ __forceinline__ int key_of_acc(int t, int r, int h) {
+    return FP8 ? 32 * h + 16 * t + r : 32 * t + 16 * (r >> 3) + 8 * h + (r & 7);
+}
+// Same map indexed by the A-operand row rho (0..31) of the score MFMA.
+template <bool FP8>
+__device__ __forceinline__ int key_of_row(int t, int rho) {
+    return key_of_acc<FP8>(t, 4 * (rho >> 3) + (rho & 3), (rho >> 2) & 1);
+}
+
+// XOR swizzle of the 16-byte chunk index of LDS key row `key`.
+template <bool FP8, int CHUNKS>
+__device__ __forceinline__ int chunk_swizzle(int key) {
+    constexpr int mask = (CHUNKS < 16 ? CHUNKS : 16) - 1;
+    const int s = FP8 ? ((key & 7) | (((key >> 5) & 1) << 3)) : (((key & 7) << 1) | ((key >> 3) & 1));
+    return s & mask;
+}
+
+// Four bf16 values (8 bytes) widened exactly from four e4m3 codes (one dword).
+__device__ __forceinline__ v2i e4m3x4_to_bf16x4(int codes) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(codes, false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(codes, true);
+    // e4m3 values are exact in bf16: keep the upper half of each f32.
+    const int w0 = (int)((__float_as_uint(lo[0]) >> 16) | (__float_as_uint(lo[1]) & 0xffff0000u));
+    const int w1 = (int)((__float_as_uint(hi[0]) >> 16) | (__float_as_uint(hi[1]) & 0xffff0000u));
+    return v2i{w0, w1};
+}
+
+// STORE8: the cache holds e4m3 (else bf16).  FP8: the MFMAs run on e4m3
+// operands (requires STORE8); otherwise they run on bf16, and an e4m3 cache
+// is widened to bf16 while it is staged into LDS.
+template <int D, bool STORE8, bool FP8>
+__global__ void __launch_bounds__(kThreads) history_fwd_kernel(FwdArgs a) {
+    static_assert(STORE8 || !FP8, "e4m3 MFMAs need an e4m3 cache");
+    constexpr int ES = FP8 ? 1 : 2;
+    constexpr int ROW = D * ES;                 // LDS bytes of one key row
+    constexpr int CHUNKS = ROW / 16;
+    constexpr int TILE = kKeyTile * ROW;        // LDS bytes of one K (or V) tile
+    constexpr int GROW = D * (STORE8 ? 1 : 2);  // cache bytes of one key row
+    constexpr int GCHUNKS = GROW / 16;
+    constexpr bool WIDEN = STORE8 && !FP8;
+    constexpr int QK = FP8 ? D / 64 : D / 16;   // k-steps of the score MFMA
+    constexpr int DT = D / 32;                  // 32-row d tiles of O^T
+    constexpr int LOADS = kKeyTile * GROW / (16 * kThreads);
+    static_assert((kKeyTile * GROW) % (16 * kThreads) == 0, "tile must split into 16-byte chunks per thread");
+
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * TILE];
+    uint8_t* const lds_k = lds;
+    uint8_t* const lds_v = lds + TILE;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 31;  // query column of the score tile / A-operand row
+    const int h = lane >> 5;  // k-group (lane half)
+    const int head = blockIdx.y;
+
+    // ---- this lane's query row -------------------------------------------
+    const int row = blockIdx.x * kRowsPerGroup + wave * kRowsPerWave + j;
+    const bool row_ok = row < a.rows_per_head;
+    const int rowc = row_ok ? row : a.rows_per_head - 1;
+    const int rank = rowc / a.group_rows;
+    const int rem = rowc - rank * a.group_rows;
+    const int head_in_group = rem / a.local_q;
+    const int tok = rem - head_in_group * a.local_q;
+    const int64_t row_off =
+        ((int64_t)(rank * a.num_q_heads + head * a.group + head_in_group) * a.local_q + tok) * D * 2;
+    const uint8_t* const qrow = a.q + row_off;
+
+    // ---- Q^T operand (register resident for the whole history) ------------
+    using QOp = typename std::conditional<FP8, v8i, v8bf>::type;
+    QOp qop[QK];
+    float cscale;
+    if constexpr (FP8) {
+        // lane (j, h) holds d = 64c + 32h + [0, 32) of its row, as e4m3.
+        float amax = 0.f;
+#pragma unroll
+        for (int c = 0; c < QK; ++c) {
+#pragma unroll
+            for (int part = 0; part < 4; ++part) {
+                const v4i raw = *(const v4i*)(qrow + (64 * c + 32 * h) * 2 + 16 * part);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const uint32_t u = (uint32_t)raw[w];
+                    amax = fmaxf(amax, fabsf(bf16_bits_to_f32(u & 0xffffu)));
+                    amax = fmaxf(amax, fabsf(bf16_bits_to_f32(u >> 16)));
+                }
+            }
+        }
+        amax = halves_max(amax);
+        const float inv = amax > 0.f ? kFp8Max / amax : 1.f;
+        const float sigma = amax > 0.f ? amax / kFp8Max : 1.f;
+#pragma unroll
+        for (int c = 0; c < QK; ++c) {
+#pragma unroll
+            for (int part = 0; part < 4; ++part) {
+                const v4i raw = *(const v4i*)(qrow + (64 * c + 32 * h) * 2 + 16 * part);
+#pragma unroll
+                for (int w = 0; w < 2; ++w) {
+                    const uint32_t u0 = (uint32_t)raw[2 * w], u1 = (uint32_t)raw[2 * w + 1];
+                    int pk = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_bits_to_f32(u0 & 0xffffu) * inv,
+                                                             bf16_bits_to_f32(u0 >> 16) * inv, 0, false);
+                    pk = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_bits_to_f32(u1 & 0xffffu) * inv,
+                                                         bf16_bits_to_f32(u1 >> 16) * inv, pk, true);
+                    qop[c][2 * part + w] = pk;
+                }
+            }
+        }
+        cscale = sigma * a.score_scale;
+    } else {
+        // lane (j, h) holds d = 16c + 8h + [0, 8) of its row.
+#pragma unroll
+        for (int c = 0; c < QK; ++c) {
+            const v4i raw = *(const v4i*)(qrow + (16 * c + 8 * h) * 2);
+            qop[c] = __builtin_bit_cast(v8bf, raw);
+        }
+        cscale = a.score_scale;
+    }
+
+    // ---- online softmax state ---------------------------------------------
+    float m_run = -INFINITY;  // running max of score * cscale (log2 domain)
+    float l_run = 0.f;        // this lane half's share of the running sum
+    v16f o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = v16f{};
+
+    // Per-lane LDS read offsets that do not depend on the tile.
+    int k_row_off[2], k_swz[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int key = key_of_row<FP8>(t, j);
+        k_row_off[t] = key * ROW;
+        k_swz[t] = chunk_swizzle<FP8, CHUNKS>(key);
+    }
+    const int grp = lane >> 4;  // 16-lane group of the transposing reads
+    const int gl = lane & 15;
+
+    for (int e = 0; e < a.num_entries; ++e) {
+        const int page = a.block_table[e];
+        const int n = min(a.page_valid_len[e], a.block_size);
+        if (n <= 0 || (unsigned)page >= (unsigned)a.num_pages) continue;
+        const uint8_t* const kpage = a.kv + (int64_t)page * a.page_stride + (int64_t)head * a.head_stride;
+        const uint8_t* const vpage = kpage + (int64_t)a.num_kv_heads * a.head_stride;
+
+        for (int base = 0; base < n; base += kKeyTile) {
+            const int valid = min(kKeyTile, n - base);
+            __syncthreads();  // previous tile fully consumed
+#pragma unroll
+            for (int i = 0; i < LOADS; ++i) {
+                const int chunk_id = tid + kThreads * i;
+                const int key = chunk_id / GCHUNKS;
+                const int ch = chunk_id - key * GCHUNKS;
+                const int64_t goff = (int64_t)(base + key) * GROW + ch * 16;
+                const v4i kc = *(const v4i*)(kpage + goff);
+                v4i vc = *(const v4i*)(vpage + goff);
+                // Masked V rows are zeroed so that 0-probability keys cannot
+                // inject NaN/Inf bit patterns from unused cache slots.
+                if (key >= valid) vc = v4i{0, 0, 0, 0};
+                const int sw = chunk_swizzle<FP8, CHUNKS>(key);
+                if constexpr (WIDEN) {
+                    // 16 e4m3 codes become 32 bytes (LDS chunks 2ch, 2ch+1).
+                    const v2i k0 = e4m3x4_to_bf16x4(kc[0]), k1 = e4m3x4_to_bf16x4(kc[1]);
+                    const v2i k2 = e4m3x4_to_bf16x4(kc[2]), k3 = e4m3x4_to_bf16x4(kc[3]);
+                    const v2i v0 = e4m3x4_to_bf16x4(vc[0]), v1 = e4m3x4_to_bf16x4(vc[1]);
+                    const v2i v2 = e4m3x4_to_bf16x4(vc[2]), v3 = e4m3x4_to_bf16x4(vc[3]);
+                    const int lo = key * ROW + (((2 * ch) ^ sw) << 4);
+                    const int hi = key * ROW + (((2 * ch + 1) ^ sw) << 4);
+                    *(v4i*)(lds_k + lo) = v4i{k0[0], k0[1], k1[0], k1[1]};
+                    *(v4i*)(lds_k + hi) = v4i{k2[0], k2[1], k3[0], k3[1]};
+                    *(v4i*)(lds_v + lo) = v4i{v0[0], v0[1], v1[0], v1[1]};
+                    *(v4i*)(lds_v + hi) = v4i{v2[0], v2[1], v3[0], v3[1]};
+                } else {
+                    const int loff = key * ROW + ((ch ^ sw) << 4);
+                    *(v4i*)(lds_k + loff) = kc;
+                    *(v4i*)(lds_v + loff) = vc;
+                }
+            }
+            __syncthreads();
+
+            // ---- S^T = K . Q^T : two 32-key x 32-query tiles --------------
+            v16f s[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                s[t] = v16f{};
+                const uint8_t* const krow = lds_k + k_row_off[t];
+#pragma unroll
+                for (int c = 0; c < QK; ++c) {
+                    if constexpr (FP8) {
+                        const v4i lo = *(const v4i*)(krow + (((4 * c + 2 * h) ^ k_swz[t]) << 4));
+                        const v4i hi = *(const v4i*)(krow + (((4 * c + 2 * h + 1) ^ k_swz[t]) << 4));
+                        const v8i aop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                        s[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, qop[c], s[t], 0, 0, 0, 0, 0, 0);
+                    } else {
+                        const v4i x = *(const v4i*)(krow + (((2 * c + h) ^ k_swz[t]) << 4));
+                        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, x), qop[c], s[t], 0, 0, 0);
+                    }
+                }
+            }
+
+            // ---- mask, online softmax ---------------------------------------
+            if (valid < kKeyTile) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (key_of_acc<FP8>(t, r, h) >= valid) s[t][r] = -INFINITY;
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+            mx = halves_max(mx);
+            const float m_new = fmaxf(m_run, mx * cscale);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            float psum = 0.f;
+            const float shift = FP8 ? kPBiasLog2 - m_new : -m_new;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], cscale, shift));
+                    s[t][r] = p;
+                    psum += p;
+                }
+            l_run = fmaf(l_run, alpha, psum);
+            m_run = m_new;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+
+            // ---- O^T += V^T . P^T ---------------------------------------------
+            if constexpr (FP8) {
+                v8i pop;
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4) {
+                        int pk = __builtin_amdgcn_cvt_pk_fp8_f32(s[t][4 * q4], s[t][4 * q4 + 1], 0, false);
+                        pk = __builtin_amdgcn_cvt_pk_fp8_f32(s[t][4 * q4 + 2], s[t][4 * q4 + 3], pk, true);
+                        pop[4 * t + q4] = pk;
+                    }
+                // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1): keys
+                // 32*(grp>>1) + [0, 32) of column d, 8 per transposing read.
+                const int vkey0 = 32 * (grp >> 1) + (gl >> 1);
+                const int vswz = chunk_swizzle<FP8, CHUNKS>(vkey0);  // same for vkey0 + 8*s
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const int chunk = (2 * dt + (grp & 1)) ^ vswz;
+                    v8i aop;
+#pragma unroll
+                    for (int s4 = 0; s4 < 4; ++s4) {
+                        const int off = (vkey0 + 8 * s4) * ROW + (chunk << 4) + 8 * (gl & 1);
+                        const v2i x = __builtin_amdgcn_ds_read_tr8_b64_v2i32(PCPA_LDS(v2i, lds_v + off));
+                        aop[2 * s4] = x[0];
+                        aop[2 * s4 + 1] = x[1];
+                    }
+                    o[dt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, pop, o[dt], 0, 0, 0, 0, 0, 0);
+                }
+            } else {
+                v8bf pop[2][2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u)
+#pragma unroll
+                        for (int e2 = 0; e2 < 8; ++e2) pop[t][u][e2] = (__bf16)s[t][8 * u + e2];
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1).
+                    const int dbyte = 2 * (32 * dt + 16 * (grp & 1) + 4 * (gl & 3));
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+#pragma unroll
+                        for (int u = 0; u < 2; ++u) {
+                            // Moved as whole dwords: element 4*s2 + b of the
+                            // operand is 16-bit half b of read s2.
+                            v4i aop;
+#pragma unroll
+                            for (int s2 = 0; s2 < 2; ++s2) {
+                                const int key = 32 * t + 16 * u + 8 * (grp >> 1) + 4 * s2 + (gl >> 2);
+                                const int off = key * ROW + (((dbyte >> 4) ^ chunk_swizzle<FP8, CHUNKS>(key)) << 4) +
+                                                (dbyte & 15);
+                                const v2i x = __builtin_bit_cast(
+                                    v2i, __builtin_amdgcn_ds_read_tr16_b64_v4i16(PCPA_LDS(v4s, lds_v + off)));
+                                aop[2 * s2] = x[0];
+                                aop[2 * s2 + 1] = x[1];
+                            }
+                            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop), pop[t][u],
+                                                                            o[dt], 0, 0, 0);
+                        }
+                }
+            }
+        }
+    }
+
+    // ---- epilogue: O = O^T / l, bf16 ---------------------------------------
+    const float l_tot = halves_sum(l_run);
+    const float scale = l_tot > 0.f ? a.v_scale / l_tot : 0.f;
+    if (row_ok) {
+        uint8_t* const orow = a.out + row_off;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int d = 32 * dt + 8 * r4 + 4 * h;
+                __bf16 v0 = (__bf16)(o[dt][4 * r4 + 0] * scale);
+                __bf16 v1 = (__bf16)(o[dt][4 * r4 + 1] * scale);
+                __bf16 v2 = (__bf16)(o[dt][4 * r4 + 2] * scale);
+                __bf16 v3 = (__bf16)(o[dt][4 * r4 + 3] * scale);
+                const uint32_t w0 = (uint32_t)__builtin_bit_cast(uint16_t, v0) |
+                                    ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16);
+                const uint32_t w1 = (uint32_t)__builtin_bit_cast(uint16_t, v2) |
+                                    ((uint32_t)__builtin_bit_cast(uint16_t, v3) << 16);
+                *(v2i*)(orow + 2 * d) = v2i{(int)w0, (int)w1};
+            }
+    }
+}
+
+}  // namespace pcpa
+
+// ============================================================================
+// C ABI
+// ============================================================================
+extern "C" {
+
+int32_t pcpa_abi_version(void) { return PCPA_ABI_VERSION; }
+
+const char* pcpa_status_string(int32_t status) {
+    switch (status) {
+        case PCPA_OK: return "ok";
+        case PCPA_ERR_NULL_POINTER: return "a required pointer is NULL";
+        case PCPA_ERR_ABI_VERSION: return "params.abi_version does not match the library";
+        case PCPA_ERR_BAD_SHAPE: return "non-positive or inconsistent sizes";
+        case PCPA_ERR_BAD_DTYPE: return "unsupported dtype code";
+        case PCPA_ERR_UNSUPPORTED: return "shape not supported by the gfx950 kernel";
+        case PCPA_ERR_MISALIGNED: return "tensor pointer is not 16-byte aligned";
+        case PCPA_ERR_LAUNCH: return "HIP kernel launch failed";
+        case PCPA_ERR_TOO_LARGE: return "sizes overflow the kernel's index arithmetic";
+        case PCPA_ERR_BAD_SCALE: return "scales must be finite and positive";
+        default: return "unknown status";
+    }
+}
+
+int32_t pcpa_check_params(const pcpa_params* p) {
+    if (p == nullptr) return PCPA_ERR_NULL_POINTER;
+    if (p->abi_version != PCPA_ABI_VERSION) return PCPA_ERR_ABI_VERSION;
+    if (p->pcp_size <= 0 || p->num_q_heads <= 0 || p->num_kv_heads <= 0 || p->head_dim <= 0 ||
+        p->local_q_len <= 0 || p->block_size <= 0 || p->max_local_blocks <= 0 || p->num_pages <= 0)
+        return PCPA_ERR_BAD_SHAPE;
+    if (p->num_q_heads % p->num_kv_heads) return PCPA_ERR_BAD_SHAPE;
+    if (p->flags & ~(uint32_t)PCPA_FLAG_BF16_MFMA) return PCPA_ERR_BAD_SHAPE;
+    if (p->q_dtype != PCPA_DTYPE_BF16 || p->out_dtype != PCPA_DTYPE_BF16) return PCPA_ERR_BAD_DTYPE;
+    if (p->kv_dtype != PCPA_DTYPE_BF16 && p->kv_dtype != PCPA_DTYPE_FP8_E4M3FN) return PCPA_ERR_BAD_DTYPE;
+    if (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256) return PCPA_ERR_UNSUPPORTED;
+    if (p->block_size % pcpa::kKeyTile) return PCPA_ERR_UNSUPPORTED;
+    if (!(isfinite(p->softmax_scale) && isfinite(p->k_scale) && isfinite(p->v_scale)) ||
+        p->softmax_scale <= 0.f || p->k_scale <= 0.f || p->v_scale <= 0.f)
+        return PCPA_ERR_BAD_SCALE;
+    const int64_t group = p->num_q_heads / p->num_kv_heads;
+    const int64_t rows = (int64_t)p->pcp_size * group * p->local_q_len;
+    const int64_t q_elems = (int64_t)p->pcp_size * p->num_q_heads * p->local_q_len * p->head_dim;
+    const int64_t entries = (int64_t)p->pcp_size * p->max_local_blocks;
+    const int64_t rank_heads = (int64_t)p->pcp_size * p->num_q_heads;
+    if (rows > INT32_MAX || entries > INT32_MAX || rank_heads > INT32_MAX || q_elems > (INT64_MAX / 4))
+        return PCPA_ERR_TOO_LARGE;
+    return PCPA_OK;
+}
+
+int32_t pcpa_history_attention(const pcpa_params* p, const void* q, const void* kv_pages,
+                               const int32_t* block_table, const int32_t* page_valid_len, void* out,
+                               void* stream) {
+    const int32_t st = pcpa_check_params(p);
+    if (st != PCPA_OK) return st;
+    if (!q || !kv_pages || !block_table || !page_valid_len || !out) return PCPA_ERR_NULL_POINTER;
+    if (((uintptr_t)q | (uintptr_t)kv_pages | (uintptr_t)out) & 15u) return PCPA_ERR_MISALIGNED;
+    if (((uintptr_t)block_table | (uintptr_t)page_valid_len) & 3u) return PCPA_ERR_MISALIGNED;
+
+    const bool store8 = p->kv_dtype == PCPA_DTYPE_FP8_E4M3FN;
+    const bool fp8 = store8 && !(p->flags & PCPA_FLAG_BF16_MFMA);
+    const int64_t es = store8 ? 1 : 2;
+    pcpa::FwdArgs a;
+    a.q = (const uint8_t*)q;
+    a.kv = (const uint8_t*)kv_pages;
+    a.block_table = block_table;
+    a.page_valid_len = page_valid_len;
+    a.out = (uint8_t*)out;
+    a.head_stride = (int64_t)p->block_size * p->head_dim * es;
+    a.page_stride = 2 * (int64_t)p->num_kv_heads * a.head_stride;
+    a.group = p->num_q_heads / p->num_kv_heads;
+    a.group_rows = a.group * p->local_q_len;
+    a.rows_per_head = p->pcp_size * a.group_rows;
+    a.local_q = p->local_q_len;
+    a.num_q_heads = p->num_q_heads;
+    a.num_kv_heads = p->num_kv_heads;
+    a.num_entries = p->pcp_size * p->max_local_blocks;
+    a.num_pages = p->num_pages;
+    a.block_size = p->block_size;
+    a.score_scale = p->softmax_scale * p->k_scale * pcpa::kLog2e;
+    a.v_scale = p->v_scale;
+
+    const dim3 grid((a.rows_per_head + pcpa::kRowsPerGroup - 1) / pcpa::kRowsPerGroup, p->num_kv_heads);
+    const dim3 block(pcpa::kThreads);
+    void* args[] = {&a};
+    const void* fn = nullptr;
+    switch (p->head_dim * 4 + (store8 ? 2 : 0) + (fp8 ? 1 : 0)) {
+        case 64 * 4 + 3: fn = (const void*)pcpa::history_fwd_kernel<64, true, true>; break;
+        case 128 * 4 + 3: fn = (const void*)pcpa::history_fwd_kernel<128, true, true>; break;
+        case 256 * 4 + 3: fn = (const void*)pcpa::history_fwd_kernel<256, true, true>; break;
+        case 64 * 4 + 2: fn = (const void*)pcpa::history_fwd_kernel<64, true, false>; break;
+        case 128 * 4 + 2: fn = (const void*)pcpa::history_fwd_kernel<128, true, false>; break;
+        case 256 * 4 + 2: fn = (const void*)pcpa::history_fwd_kernel<256, true, false>; break;
+        case 64 * 4: fn = (const void*)pcpa::history_fwd_kernel<64, false, false>; break;
+        case 128 * 4: fn = (const void*)pcpa::history_fwd_kernel<128, false, false>; break;
+        case 256 * 4: fn = (const void*)pcpa::history_fwd_kernel<256, false, false>; break;
+        default: return PCPA_ERR_UNSUPPORTED;
+    }
+    const hipError_t err = hipLaunchKernel(fn, grid, block, args, 0, (hipStream_t)stream);
+    return err == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
+}
+
+}  // extern "C"

@@ -1,0 +1,218 @@
+"""HIP (gfx950) implementation of history-only PCP attention.
+
+Same public names as ``pcp_attention/kernel.py`` of the Trainium2 proof of
+concept: ``pack_local_kv`` (kernel.py:17-29), ``make_history_attention_kernel``
+(kernel.py:32-556) and ``wrap_for_native_torch`` (kernel.py:559-564).  The
+device code is a hand-written gfx950 kernel in
+``aws_training_study_amd/csrc/pcp_attention_hip.hip`` reached through its C
+ABI (``include/pcp_attention_hip.h``) with ctypes; there is no other
+execution path, and a missing library raises.
+
+Difference in calling convention: the reference kernel runs once per
+logical rank and circulates KV blocks around a device ring.  Here one call
+takes every rank's Q stacked as ``[pcp, Hq, local_q, D]`` plus the paged pool
+of every rank's packed KV blocks and a block table, and returns every rank's
+output ``[pcp, Hq, local_q, D]`` (``out[r]`` is the reference's rank-``r``
+output).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import replace
+from typing import Any
+
+from .config import PCPAttentionConfig
+
+
+def pack_local_kv(k: Any, v: Any) -> Any:
+    """Pack ``[blocks, Hkv, block_size, D]`` K and V into one row per block.
+
+    Row ``b`` holds all of block ``b``'s K followed by all of its V, so it
+    reshapes to ``[2, Hkv, block_size, D]``.  The dtype is kept (FP8 stays one
+    byte per element).
+    """
+    import torch
+
+    if k.shape != v.shape or k.ndim != 4:
+        raise ValueError("K and V must have equal [blocks, Hkv, block, D] shapes")
+    blocks = k.shape[0]
+    packed = torch.empty((blocks, 2, *k.shape[1:]), dtype=k.dtype, device=k.device)
+    packed[:, 0] = k
+    packed[:, 1] = v
+    return packed.reshape(blocks, -1)
+
+
+_KV_DTYPE_CODES = {"fp8_e4m3fn": 2, "bfloat16": 1}
+
+PRECISIONS = ("auto", "fp8", "bf16")
+# Below this many valid history tokens, ``precision="auto"`` runs an e4m3
+# cache through BF16 MFMAs: e4m3 rounding of Q and P is noise that is only
+# averaged away over many keys (at 785 tokens it reaches a 2e-2 max error).
+AUTO_BF16_BELOW_TOKENS = 2048
+
+
+def _torch_kv_dtype(name: str):
+    import torch
+
+    return {"fp8_e4m3fn": torch.float8_e4m3fn, "bfloat16": torch.bfloat16}[name]
+
+
+class HistoryAttentionKernel:
+    """Callable launching the gfx950 history attention kernel.
+
+    ``kernel(q, kv_pages, block_table, block_valid_mask=None, *,
+    page_valid_len=None, k_scale=1.0, v_scale=1.0, out=None) -> out``
+
+    * ``q``: ``[pcp, Hq, local_q, D]`` bfloat16 on the GPU (every rank's Q
+      shard, ``layout.stacked_query``).
+    * ``kv_pages``: ``[num_pages, 2 * Hkv * block_size * D]`` in the config's
+      ``kv_dtype``; row ``p`` is a ``pack_local_kv`` row.
+    * ``block_table``: int ``[pcp, max_local_blocks]`` page of each cache block.
+    * validity: ``page_valid_len`` (int ``[pcp, max_local_blocks]``), or the
+      reference's ``block_valid_mask`` (run_poc.py:137-153, shared by all
+      ranks), or neither, in which case the config's ``actual_history_len``
+      decides.
+    * ``k_scale``/``v_scale``: per-tensor dequantisation scales of K and V.
+    * ``precision``: for an e4m3 cache, ``"fp8"`` runs both GEMMs as e4m3
+      MFMAs (Q and P rounded to e4m3), ``"bf16"`` as BF16 MFMAs on the exactly
+      widened cache, and ``"auto"`` picks ``"bf16"`` when the config's
+      ``actual_history_len`` is below ``AUTO_BF16_BELOW_TOKENS``.
+
+    The launch is asynchronous on the current torch stream.
+    """
+
+    def __init__(self, config: PCPAttentionConfig):
+        from .. import _native
+
+        self.config = replace(config, backend="hip").validate()
+        self._native = _native
+        self._lib = _native.load_library()
+        cfg = self.config
+        self._static = dict(
+            abi_version=_native.ABI_VERSION,
+            pcp_size=cfg.pcp_size,
+            num_q_heads=cfg.num_q_heads,
+            num_kv_heads=cfg.num_kv_heads,
+            head_dim=cfg.head_dim,
+            local_q_len=cfg.local_q_len,
+            block_size=cfg.block_size,
+            max_local_blocks=cfg.max_local_blocks,
+            q_dtype=_native.DTYPE_BF16,
+            kv_dtype=_KV_DTYPE_CODES[cfg.kv_dtype],
+            out_dtype=_native.DTYPE_BF16,
+            softmax_scale=cfg.softmax_scale,
+            flags=0,
+        )
+        status = self._lib.pcpa_check_params(ctypes.byref(self._params(cfg.num_pages, 1.0, 1.0)))
+        if status != _native.PCPA_OK:
+            raise ValueError(f"configuration rejected by the HIP kernel: {_native.status_string(status)}")
+        self._default_valid = None
+
+    def _params(self, num_pages: int, k_scale: float, v_scale: float):
+        return self._native.PcpaParams(
+            num_pages=num_pages, k_scale=float(k_scale), v_scale=float(v_scale), **self._static
+        )
+
+    def uses_bf16_mfma(self, precision: str = "auto") -> bool:
+        """Whether a call with ``precision`` runs BF16 MFMAs."""
+        if self.config.kv_dtype != "fp8_e4m3fn" or precision == "bf16":
+            return True
+        if precision == "fp8":
+            return False
+        return self.config.actual_history_len < AUTO_BF16_BELOW_TOKENS
+
+    def default_page_valid_len(self, device) -> Any:
+        from .paging import page_valid_lengths
+
+        if self._default_valid is None or self._default_valid.device != device:
+            self._default_valid = page_valid_lengths(self.config).to(device)
+        return self._default_valid
+
+    def __call__(
+        self,
+        q,
+        kv_pages,
+        block_table,
+        block_valid_mask=None,
+        *,
+        page_valid_len=None,
+        k_scale: float = 1.0,
+        v_scale: float = 1.0,
+        out=None,
+        precision: str = "auto",
+    ):
+        import torch
+
+        cfg = self.config
+        if precision not in PRECISIONS:
+            raise ValueError(f"precision must be one of {PRECISIONS}, got {precision!r}")
+        if not q.is_cuda:
+            raise ValueError("q must be a GPU tensor")
+        device = q.device
+        q_shape = (cfg.pcp_size, cfg.num_q_heads, cfg.local_q_len, cfg.head_dim)
+        if tuple(q.shape) != q_shape or q.dtype != torch.bfloat16 or not q.is_contiguous():
+            raise ValueError(f"q must be contiguous bfloat16 {q_shape}, got {q.dtype} {tuple(q.shape)}")
+        kv_dtype = _torch_kv_dtype(cfg.kv_dtype)
+        if (
+            kv_pages.ndim != 2
+            or kv_pages.shape[1] != cfg.page_elements
+            or kv_pages.dtype != kv_dtype
+            or not kv_pages.is_contiguous()
+            or kv_pages.device != device
+        ):
+            raise ValueError(
+                f"kv_pages must be contiguous {kv_dtype} [num_pages, {cfg.page_elements}] on {device}, "
+                f"got {kv_pages.dtype} {tuple(kv_pages.shape)} on {kv_pages.device}"
+            )
+        num_pages = kv_pages.shape[0]
+        table_shape = (cfg.pcp_size, cfg.max_local_blocks)
+        if tuple(block_table.shape) != table_shape:
+            raise ValueError(f"block_table must be {table_shape}, got {tuple(block_table.shape)}")
+        block_table = block_table.to(device=device, dtype=torch.int32).contiguous()
+        if page_valid_len is not None and block_valid_mask is not None:
+            raise ValueError("pass either page_valid_len or block_valid_mask, not both")
+        if page_valid_len is None:
+            if block_valid_mask is not None:
+                from .paging import valid_lengths_from_block_mask
+
+                page_valid_len = valid_lengths_from_block_mask(block_valid_mask, cfg)
+            else:
+                page_valid_len = self.default_page_valid_len(device)
+        if tuple(page_valid_len.shape) != table_shape:
+            raise ValueError(f"page_valid_len must be {table_shape}, got {tuple(page_valid_len.shape)}")
+        page_valid_len = page_valid_len.to(device=device, dtype=torch.int32).contiguous()
+        if out is None:
+            out = torch.empty(q_shape, dtype=torch.bfloat16, device=device)
+        elif tuple(out.shape) != q_shape or out.dtype != torch.bfloat16 or not out.is_contiguous() or out.device != device:
+            raise ValueError(f"out must be contiguous bfloat16 {q_shape} on {device}")
+        params = self._params(num_pages, k_scale, v_scale)
+        if self.uses_bf16_mfma(precision):
+            params.flags = self._native.FLAG_BF16_MFMA
+        with torch.cuda.device(device):
+            stream = torch.cuda.current_stream(device).cuda_stream
+            status = self._lib.pcpa_history_attention(
+                ctypes.byref(params),
+                q.data_ptr(),
+                kv_pages.data_ptr(),
+                block_table.data_ptr(),
+                page_valid_len.data_ptr(),
+                out.data_ptr(),
+                stream,
+            )
+        self._native.check(status)
+        return out
+
+
+def make_history_attention_kernel(config: PCPAttentionConfig) -> HistoryAttentionKernel:
+    """Build the gfx950 kernel callable for ``config``.
+
+    Raises ``ValueError`` for shapes the HIP kernel does not support (the
+    reference raises for shapes its NKI kernel does not, kernel.py:42-51).
+    """
+    return HistoryAttentionKernel(config)
+
+
+def wrap_for_native_torch(config: PCPAttentionConfig) -> HistoryAttentionKernel:
+    """Torch-callable kernel; the HIP callable already takes torch tensors."""
+    return make_history_attention_kernel(config)

@@ -1,0 +1,207 @@
+#!/usr/bin/env python3
+"""Benchmark of history-only PCP attention on one MI355X.
+
+Default workload: 64 logical PCP ranks, 4096 current tokens attending a
+131072-token paged FP8 (e4m3, per-tensor scale) history, 32 Q / 2 KV heads,
+D 256, 512-token blocks, interleave 64, seeded random block table.  A step is
+one launch of the gfx950 kernel over all ranks with every input resident in
+HBM.  Prints one JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--workload NAME]
+
+``value`` is model TFLOP/s (4 * Hq * Q * L_valid * D per step, the
+reference's definition, README.md:167-171) from the wall time of the K timed
+steps; ``roofline`` prices the kernel's own HIP-event duration against the
+MI355X dense MFMA peak; ``cpu_baseline`` times the CPU ring model (the
+oracle's restatement of reference.py:35-95) on a bounded sample of ranks.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "ms + TFLOP/s (% FP8 MFMA peak), Q=4K x 128K paged FP8 KV history, 1 GPU"
+# MI355X published dense MFMA peaks, TFLOP/s.
+PEAK_TFLOPS = {"fp8_e4m3fn": 5000.0, "bfloat16": 2500.0}
+HBM_PEAK_GBS = 8000.0
+
+
+def parse_args(argv=None):
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[1])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=30)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--workload", default="full-fp8")
+    parser.add_argument("--seed", type=int, default=1234)
+    parser.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
+                        help="approximate CPU time budget of the ring-model baseline sample")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    return parser.parse_args(argv)
+
+
+def model_flops(cfg) -> float:
+    return 4.0 * cfg.num_q_heads * cfg.current_len * cfg.actual_history_len * cfg.head_dim
+
+
+def algorithmic_bytes(cfg) -> float:
+    """Q in + O out + valid K/V + block table + valid lengths."""
+    q = 2.0 * cfg.num_q_heads * cfg.current_len * cfg.head_dim
+    kv = 2.0 * cfg.num_kv_heads * cfg.actual_history_len * cfg.head_dim * cfg.kv_element_size
+    tables = 2 * 4.0 * cfg.num_pages
+    return 2 * q + kv + tables
+
+
+def cpu_baseline(problem, budget_s: float) -> dict:
+    """Time the oracle's CPU ring model on the first k ranks and extrapolate."""
+    import torch
+
+    from aws_training_study_amd.pcp_attention.layout import shard_history, shard_query
+    from oracle import pcp_oracle as orc
+
+    cfg = problem.config
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    shape = orc.OracleShape.from_config(cfg)
+    q_shards = shard_query(problem.inputs.q, cfg)
+    k_shards, v_shards = shard_history(problem.inputs.k, problem.inputs.v, cfg)
+    start = time.perf_counter()
+    orc.ring_history_attention(q_shards[:1], k_shards, v_shards, shape)
+    per_rank = time.perf_counter() - start
+    ranks = 1
+    extra = min(cfg.pcp_size - 1, int(max(0.0, budget_s - per_rank) / max(per_rank, 1e-9)))
+    if extra > 0:
+        start = time.perf_counter()
+        orc.ring_history_attention(q_shards[1:1 + extra], k_shards, v_shards, shape)
+        elapsed = time.perf_counter() - start
+        per_rank = (per_rank + elapsed) / (1 + extra)
+        ranks += extra
+    full_s = per_rank * cfg.pcp_size
+    return {
+        "value": model_flops(cfg) / full_s / 1e12,
+        "unit": "TFLOP/s",
+        "ms": full_s * 1e3,
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            f"ring model (reference.py:35-95 loop order, FP32 torch on {threads} host threads) "
+            f"over {ranks} of {cfg.pcp_size} ranks, full history each; every rank does identical "
+            f"work, time extrapolated x{cfg.pcp_size / ranks:g}"
+        ),
+    }
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(
+            f"bench.py runs on one GPU only: the collapsed PCP path keeps every rank's pages in one "
+            f"GPU's HBM and has no multi-GPU mode (asked for --gpus {args.gpus})",
+            file=sys.stderr,
+        )
+        return 2
+    if args.steps < 1 or args.warmup < 1:
+        print("--steps and --warmup must be at least 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from aws_training_study_amd.pcp_attention import make_history_attention_kernel
+    from aws_training_study_amd.pcp_attention.workloads import build_workload_problem, get_workload
+
+    workload = get_workload(args.workload)
+    problem = build_workload_problem(workload, args.seed)
+    cfg = problem.config
+    device = torch.device("cuda", 0)
+    gpu = problem.to(device)
+    kernel = make_history_attention_kernel(cfg)
+    out = torch.empty_like(gpu.q_stacked)
+
+    def step():
+        kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len,
+               k_scale=problem.k_scale, v_scale=problem.v_scale, out=out)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Timed region: exactly K steps, synchronised on both sides.
+    stream = torch.cuda.current_stream(device)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for begin, end in events:
+        begin.record(stream)
+        step()
+        end.record(stream)
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    launch_ms = sorted(b.elapsed_time(e) for b, e in events)
+
+    flops = model_flops(cfg)
+    ms_per_step = wall_s * 1e3 / args.steps
+    kernel_ms = statistics.fmean(launch_ms)
+    peak = PEAK_TFLOPS[cfg.kv_dtype]
+    achieved = flops / (kernel_ms * 1e-3) / 1e12
+    p90 = launch_ms[max(0, (9 * len(launch_ms) + 9) // 10 - 1)]
+
+    result = {
+        "metric": METRIC,
+        "value": round(flops / (ms_per_step * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3" if cfg.kv_dtype == "fp8_e4m3fn" else "bf16",
+        "data": "synthetic (seeded N(0,1) BF16 Q, K/V quantised to e4m3 with per-tensor amax/448 scales)",
+        "config": {
+            "workload": workload.name,
+            "pcp_ranks": cfg.pcp_size,
+            "current_tokens": cfg.current_len,
+            "history_tokens": cfg.actual_history_len,
+            "q_heads": cfg.num_q_heads,
+            "kv_heads": cfg.num_kv_heads,
+            "head_dim": cfg.head_dim,
+            "block_size": cfg.block_size,
+            "interleave": cfg.interleave_size,
+            "kv_dtype": cfg.kv_dtype,
+        },
+        "pct_peak": round(100.0 * flops / (ms_per_step * 1e-3) / 1e12 / peak, 2),
+        "kernel_ms": {
+            "min": round(launch_ms[0], 4),
+            "median": round(statistics.median(launch_ms), 4),
+            "mean": round(kernel_ms, 4),
+            "p90": round(p90, 4),
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4),
+            "traffic": None,
+            "algorithmic_bytes": algorithmic_bytes(cfg),
+            "algorithmic_hbm_gbs": round(algorithmic_bytes(cfg) / (kernel_ms * 1e-3) / 1e9, 1),
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(problem, args.cpu_baseline_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,121 @@
+/*
+ * C ABI of the MI355X (gfx950) history-only PCP attention library
+ * (libpcp_attention_hip.so).
+ *
+ * Plain C types only: device pointers are `const void*` / `void*`, the HIP
+ * stream is passed as `void*` (a hipStream_t, or NULL for the null stream).
+ * The library never allocates device memory and never synchronises the
+ * host: every launch is asynchronous on the given stream.  Calls are
+ * stateless and re-entrant (safe from several host threads on different
+ * streams).  Status codes are returned, never printed.
+ *
+ * Reference interface replaced (Trainium2 NKI proof of concept):
+ *   pcp_attention/kernel.py:32-556  make_history_attention_kernel(config)
+ *       -> history_attention_kernel(q_ref, local_kv_ref, block_valid_mask_ref)
+ *   pcp_attention/kernel.py:559-564 wrap_for_native_torch(config)
+ * The reference runs one kernel instance per logical PCP rank and rotates
+ * KV blocks around a device ring (kernel.py:276-293).  Here every rank's
+ * KV blocks sit in one paged pool in HBM and one launch computes all
+ * ranks' outputs; the ring becomes a loop over the block table.
+ */
+#ifndef PCP_ATTENTION_HIP_H
+#define PCP_ATTENTION_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PCPA_ABI_VERSION 1
+
+/* Status codes. */
+#define PCPA_OK 0
+#define PCPA_ERR_NULL_POINTER (-1)  /* a required pointer is NULL            */
+#define PCPA_ERR_ABI_VERSION (-2)   /* params.abi_version != PCPA_ABI_VERSION */
+#define PCPA_ERR_BAD_SHAPE (-3)     /* non-positive or inconsistent sizes     */
+#define PCPA_ERR_BAD_DTYPE (-4)     /* dtype code not supported              */
+#define PCPA_ERR_UNSUPPORTED (-5)   /* valid but not implemented (head_dim…) */
+#define PCPA_ERR_MISALIGNED (-6)    /* a tensor pointer is not 16-byte aligned */
+#define PCPA_ERR_LAUNCH (-7)        /* the HIP launch itself failed          */
+#define PCPA_ERR_TOO_LARGE (-8)     /* an index would overflow 32/64-bit maths */
+#define PCPA_ERR_BAD_SCALE (-9)     /* a scale is not finite and positive    */
+
+/* params.flags bits. */
+/* Run both GEMMs as BF16 MFMAs even for an e4m3 cache: K/V are widened to
+ * bf16 exactly while staged, Q and P stay bf16.  Half the MFMA rate, but no
+ * e4m3 rounding of Q and P (which matters for short histories, where that
+ * noise is not averaged over many keys).  Ignored for a bf16 cache. */
+#define PCPA_FLAG_BF16_MFMA 1u
+
+/* dtype codes. */
+#define PCPA_DTYPE_BF16 1
+#define PCPA_DTYPE_FP8_E4M3FN 2 /* OCP e4m3 "fn": bias 7, max 448, no inf */
+
+/*
+ * Shapes of one launch.  All ranks are processed together.
+ *   q            [pcp_size, num_q_heads, local_q_len, head_dim]   q_dtype
+ *   kv_pages     [num_pages, 2, num_kv_heads, block_size, head_dim] kv_dtype
+ *                (each row is pack_local_kv's payload, kernel.py:17-29:
+ *                 all K of a block, then all V)
+ *   block_table  [pcp_size, max_local_blocks] int32: physical page of
+ *                (rank, local block); entries outside [0, num_pages) are
+ *                treated as empty pages (never read)
+ *   page_valid_len [pcp_size, max_local_blocks] int32: number of valid
+ *                leading tokens of that cache block, clamped to
+ *                [0, block_size].  Valid tokens of a striped rank always
+ *                form a prefix of its local sequence, so this encodes the
+ *                reference's additive mask (run_poc.py:137-153) exactly.
+ *   out          [pcp_size, num_q_heads, local_q_len, head_dim] bf16
+ * Q heads are grouped contiguously per KV head: Q head h reads KV head
+ * h / (num_q_heads / num_kv_heads) (reference.py:10-13).
+ * Scores are (q . k) * softmax_scale * k_scale; V is multiplied by v_scale
+ * (per-tensor dequantisation scales, 1.0 for unscaled storage).
+ */
+typedef struct pcpa_params {
+    int32_t abi_version;
+    int32_t pcp_size;
+    int32_t num_q_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t local_q_len;
+    int32_t block_size;
+    int32_t max_local_blocks;
+    int32_t num_pages;
+    int32_t q_dtype;
+    int32_t kv_dtype;
+    int32_t out_dtype;
+    float softmax_scale;
+    float k_scale;
+    float v_scale;
+    uint32_t flags; /* PCPA_FLAG_* bits; other bits must be 0 */
+} pcpa_params;
+
+/* Returns PCPA_ABI_VERSION of the loaded library. */
+int32_t pcpa_abi_version(void);
+
+/* Static, NUL-terminated description of a status code. */
+const char* pcpa_status_string(int32_t status);
+
+/*
+ * Validate `params` without launching anything (no HIP call is made).
+ * Returns PCPA_OK or the error the launch entry point would return for
+ * these parameters (pointer checks excluded).
+ */
+int32_t pcpa_check_params(const pcpa_params* params);
+
+/*
+ * History-only attention over the paged KV pool for every rank's Q.
+ * Replaces kernel.py:32-556 (history_attention_kernel) and
+ * kernel.py:559-564 (wrap_for_native_torch).  Output is caller-allocated
+ * (the reference kernel allocated it, kernel.py:124).
+ */
+int32_t pcpa_history_attention(const pcpa_params* params, const void* q, const void* kv_pages,
+                               const int32_t* block_table, const int32_t* page_valid_len,
+                               void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PCP_ATTENTION_HIP_H */

@@ -1,0 +1,108 @@
+"""C ABI of libpcp_attention_hip.so without a GPU: the library loads, exports every
+symbol include/pcp_attention_hip.h declares, and rejects bad parameters before
+any HIP call."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from aws_training_study_amd import _native
+from aws_training_study_amd.pcp_attention import make_history_attention_kernel
+from aws_training_study_amd.pcp_attention.config import PCPAttentionConfig
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "pcp_attention_hip.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _native.library_path().exists():
+        pytest.fail("libpcp_attention_hip.so is not built; run __graft_entry__.build()")
+    return _native.load_library()
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int32_t|const char\*)\s+(pcpa_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_what_python_binds():
+    assert _declared_functions() == sorted(_native.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_status_codes_match_header(lib):
+    text = HEADER.read_text()
+    codes = {name: int(value) for name, value in re.findall(r"#define (PCPA_(?:OK|ERR_\w+))\s+\(?(-?\d+)\)?", text)}
+    assert codes["PCPA_OK"] == 0
+    for name, value in codes.items():
+        assert _native.STATUS_NAMES[value] == name
+        assert lib.pcpa_status_string(value).decode() != "unknown status"
+    assert lib.pcpa_abi_version() == _native.ABI_VERSION
+    assert f"#define PCPA_ABI_VERSION {_native.ABI_VERSION}" in text
+
+
+def test_params_struct_layout():
+    text = HEADER.read_text()
+    body = re.search(r"typedef struct pcpa_params \{(.*?)\} pcpa_params;", text, re.S).group(1)
+    fields = re.findall(r"(?:int32_t|uint32_t|float)\s+(\w+);", body)
+    assert fields == [name for name, _ in _native.PcpaParams._fields_]
+    assert ctypes.sizeof(_native.PcpaParams) == 4 * len(fields)
+
+
+def _good_params(**kw):
+    p = dict(abi_version=1, pcp_size=4, num_q_heads=8, num_kv_heads=2, head_dim=64, local_q_len=64,
+             block_size=128, max_local_blocks=4, num_pages=16, q_dtype=1, kv_dtype=1, out_dtype=1,
+             softmax_scale=0.125, k_scale=1.0, v_scale=1.0, flags=0)
+    p.update(kw)
+    return _native.PcpaParams(**p)
+
+
+@pytest.mark.parametrize(
+    "change,status",
+    [
+        ({}, 0),
+        ({"abi_version": 2}, -2),
+        ({"pcp_size": 0}, -3),
+        ({"num_q_heads": 7}, -3),
+        ({"flags": 1}, 0),
+        ({"flags": 2}, -3),
+        ({"q_dtype": 2}, -4),
+        ({"kv_dtype": 9}, -4),
+        ({"head_dim": 96}, -5),
+        ({"block_size": 96}, -5),
+        ({"softmax_scale": 0.0}, -9),
+        ({"v_scale": float("nan")}, -9),
+        ({"pcp_size": 1 << 20, "local_q_len": 1 << 12}, -8),
+    ],
+)
+def test_check_params(lib, change, status):
+    assert lib.pcpa_check_params(ctypes.byref(_good_params(**change))) == status
+
+
+def test_launch_rejects_null_and_misaligned_pointers_without_a_gpu(lib):
+    p = _good_params()
+    assert lib.pcpa_history_attention(None, 16, 16, 16, 16, 16, None) == -1
+    assert lib.pcpa_history_attention(ctypes.byref(p), None, 16, 16, 16, 16, None) == -1
+    assert lib.pcpa_history_attention(ctypes.byref(p), 16, 16, 16, 16, 0, None) == -1
+    assert lib.pcpa_history_attention(ctypes.byref(p), 8, 16, 16, 16, 16, None) == -6
+    assert lib.pcpa_history_attention(ctypes.byref(p), 16, 16, 2, 16, 16, None) == -6
+    bad = _good_params(head_dim=96)
+    assert lib.pcpa_history_attention(ctypes.byref(bad), 16, 16, 16, 16, 16, None) == -5
+
+
+def test_python_entry_validates_before_launch():
+    with pytest.raises(ValueError, match="head_dim must be one of"):
+        make_history_attention_kernel(PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=2048,
+                                                         actual_history_len=2048, head_dim=384))
+    kernel = make_history_attention_kernel(PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=2048,
+                                                              actual_history_len=2048, backend="hip"))
+    q = torch.zeros(4, 32, 64, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        kernel(q, torch.zeros(4, 10), torch.zeros(4, 1, dtype=torch.int32))
