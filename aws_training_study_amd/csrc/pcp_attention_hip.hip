@@ -68,6 +68,7 @@ struct FwdArgs {
     int64_t page_stride;   // bytes of one page (K and V of every KV head)
     int64_t head_stride;   // bytes of one head's K (or V) block
     int32_t rows_per_head; // pcp * group * local_q
+    int32_t row_tiles;     // ceil(rows_per_head / kRowsPerGroup)
     int32_t group_rows;    // group * local_q
     int32_t local_q;
     int32_t num_q_heads;
@@ -129,37 +130,184 @@ __device__ __forceinline__ v2i e4m3x4_to_bf16x4(int codes) {
     return v2i{w0, w1};
 }
 
+// s_waitcnt vmcnt(0) with expcnt/lgkmcnt left unconstrained (gfx9 encoding).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Transposing LDS reads as inline asm.  The builtins carry no memory-operand
+// information, so the compiler orders them after every in-flight LDS DMA,
+// including the prefetch of the *other* buffer, which would serialise the
+// pipeline.  Ordering against this buffer's DMA is provided by the
+// vmcnt(0) + barrier at the top of each tile; the caller makes the results
+// usable with lds_results_ready().
+__device__ __forceinline__ uint32_t lds_address(const uint8_t* p) {
+    return (uint32_t)(uintptr_t)PCPA_LDS(const uint8_t, p);
+}
+__device__ __forceinline__ v2i ds_read_tr8_b64(uint32_t addr) {
+    v2i r;
+    asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(r) : "v"(addr));
+    return r;
+}
+__device__ __forceinline__ v2i ds_read_tr16_b64(uint32_t addr) {
+    v2i r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr));
+    return r;
+}
+// s_waitcnt lgkmcnt(0), with the read results as operands so that no use of
+// them can be scheduled before the wait.
+__device__ __forceinline__ void lds_results_ready(v2i& a, v2i& b, v2i& c, v2i& d) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
+__device__ __forceinline__ void lds_results_ready(v2i& a, v2i& b) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b));
+}
+
+// Position in the walk over the block table: entry e (rank-major (rank,
+// block) order), tile start `base` within the page, the page's valid length
+// n, and the byte offset of this KV head's K block in the pool.
+struct TileCursor {
+    int e;
+    int base;
+    int n;
+    int64_t k_off;
+};
+
+// The tile after `c`: the next 64 keys of the same page, or the first tile
+// of the next table entry with valid tokens and an in-range page.  Entries
+// whose page index is outside [0, num_pages) are never read.
+__device__ __forceinline__ TileCursor next_tile(const FwdArgs& a, int head, TileCursor c) {
+    if (c.base + kKeyTile < c.n) {
+        c.base += kKeyTile;
+        return c;
+    }
+    for (int e = c.e + 1; e < a.num_entries; ++e) {
+        const int page = a.block_table[e];
+        const int n = min(a.page_valid_len[e], a.block_size);
+        if (n > 0 && (unsigned)page < (unsigned)a.num_pages)
+            return TileCursor{e, 0, n, (int64_t)page * a.page_stride + (int64_t)head * a.head_stride};
+    }
+    return TileCursor{a.num_entries, 0, 0, 0};
+}
+
 // STORE8: the cache holds e4m3 (else bf16).  FP8: the MFMAs run on e4m3
 // operands (requires STORE8); otherwise they run on bf16, and an e4m3 cache
 // is widened to bf16 while it is staged into LDS.
 template <int D, bool STORE8, bool FP8>
-__global__ void __launch_bounds__(kThreads) history_fwd_kernel(FwdArgs a) {
+struct TileShape {
     static_assert(STORE8 || !FP8, "e4m3 MFMAs need an e4m3 cache");
-    constexpr int ES = FP8 ? 1 : 2;
-    constexpr int ROW = D * ES;                 // LDS bytes of one key row
-    constexpr int CHUNKS = ROW / 16;
-    constexpr int TILE = kKeyTile * ROW;        // LDS bytes of one K (or V) tile
-    constexpr int GROW = D * (STORE8 ? 1 : 2);  // cache bytes of one key row
-    constexpr int GCHUNKS = GROW / 16;
-    constexpr bool WIDEN = STORE8 && !FP8;
-    constexpr int QK = FP8 ? D / 64 : D / 16;   // k-steps of the score MFMA
-    constexpr int DT = D / 32;                  // 32-row d tiles of O^T
-    constexpr int LOADS = kKeyTile * GROW / (16 * kThreads);
-    static_assert((kKeyTile * GROW) % (16 * kThreads) == 0, "tile must split into 16-byte chunks per thread");
+    static constexpr int ES = FP8 ? 1 : 2;
+    static constexpr int ROW = D * ES;                 // LDS bytes of one key row
+    static constexpr int CHUNKS = ROW / 16;
+    static constexpr int TILE = kKeyTile * ROW;        // LDS bytes of one K (or V) tile
+    static constexpr int GROW = D * (STORE8 ? 1 : 2);  // cache bytes of one key row
+    static constexpr int GCHUNKS = GROW / 16;
+    static constexpr bool WIDEN = STORE8 && !FP8;
+    // Double-buffered (prefetching) when both buffers fit the 64 KB static
+    // LDS limit; the widening path stages synchronously through registers.
+    static constexpr int NBUF = (!WIDEN && 4 * TILE <= 65536) ? 2 : 1;
+    static constexpr int QK = FP8 ? D / 64 : D / 16;   // k-steps of the score MFMA
+    static constexpr int DT = D / 32;                  // 32-row d tiles of O^T
+    // Lazy rescale: the running max is only raised when a tile's max exceeds
+    // it by more than this (log2 units); FP8 probabilities then stay below
+    // 2^(kPBiasLog2 + 2.5) = 362 < 448.
+    static constexpr float RESCALE_LOG2 = FP8 ? 2.5f : 8.0f;
+};
 
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * TILE];
-    uint8_t* const lds_k = lds;
-    uint8_t* const lds_v = lds + TILE;
+// Issue asynchronous global->LDS loads of one 64-key K tile and V tile.  The
+// tile is split into 1024-byte blocks; each wave loads CHUNKS/4 blocks of
+// each, one 16-byte chunk per lane, landing at block + 16 * lane.  The lane's
+// global chunk is chosen so that the swizzled LDS layout comes out.
+template <class S>
+__device__ __forceinline__ void stage_tile_async(const FwdArgs& a, const TileCursor& c, uint8_t* lds_k,
+                                                 uint8_t* lds_v, int wave, int lane) {
+    constexpr int BLOCKS_PER_WAVE = S::CHUNKS / 4;
+    const uint8_t* const kpage = a.kv + c.k_off;
+    const uint8_t* const vpage = kpage + (int64_t)a.num_kv_heads * a.head_stride;
+#pragma unroll
+    for (int i = 0; i < BLOCKS_PER_WAVE; ++i) {
+        const int block = wave * BLOCKS_PER_WAVE + i;
+        const int byte = block * 1024 + lane * 16;
+        const int key = byte / S::ROW;
+        const int pos = (byte % S::ROW) / 16;
+        const int chunk = pos ^ chunk_swizzle<S::ES == 1, S::CHUNKS>(key);
+        const int64_t goff = (int64_t)(c.base + key) * S::GROW + chunk * 16;
+        __builtin_amdgcn_global_load_lds(kpage + goff, PCPA_LDS(void, lds_k + block * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vpage + goff, PCPA_LDS(void, lds_v + block * 1024), 16, 0, 0);
+    }
+}
+
+// Synchronous staging through registers, widening e4m3 to bf16 when the
+// MFMAs are bf16.  Rows at or beyond `valid` get zero V.
+template <class S>
+__device__ __forceinline__ void stage_tile_sync(const FwdArgs& a, const TileCursor& c, int valid, uint8_t* lds_k,
+                                                uint8_t* lds_v, int tid) {
+    constexpr int LOADS = kKeyTile * S::GROW / (16 * kThreads);
+    static_assert((kKeyTile * S::GROW) % (16 * kThreads) == 0, "tile must split into 16-byte chunks per thread");
+    const uint8_t* const kpage = a.kv + c.k_off;
+    const uint8_t* const vpage = kpage + (int64_t)a.num_kv_heads * a.head_stride;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int chunk_id = tid + kThreads * i;
+        const int key = chunk_id / S::GCHUNKS;
+        const int ch = chunk_id - key * S::GCHUNKS;
+        const int64_t goff = (int64_t)(c.base + key) * S::GROW + ch * 16;
+        const v4i kc = *(const v4i*)(kpage + goff);
+        v4i vc = *(const v4i*)(vpage + goff);
+        if (key >= valid) vc = v4i{0, 0, 0, 0};
+        const int sw = chunk_swizzle<S::ES == 1, S::CHUNKS>(key);
+        if constexpr (S::WIDEN) {
+            // 16 e4m3 codes become 32 bytes (LDS chunks 2ch, 2ch+1).
+            const v2i k0 = e4m3x4_to_bf16x4(kc[0]), k1 = e4m3x4_to_bf16x4(kc[1]);
+            const v2i k2 = e4m3x4_to_bf16x4(kc[2]), k3 = e4m3x4_to_bf16x4(kc[3]);
+            const v2i v0 = e4m3x4_to_bf16x4(vc[0]), v1 = e4m3x4_to_bf16x4(vc[1]);
+            const v2i v2 = e4m3x4_to_bf16x4(vc[2]), v3 = e4m3x4_to_bf16x4(vc[3]);
+            const int lo = key * S::ROW + (((2 * ch) ^ sw) << 4);
+            const int hi = key * S::ROW + (((2 * ch + 1) ^ sw) << 4);
+            *(v4i*)(lds_k + lo) = v4i{k0[0], k0[1], k1[0], k1[1]};
+            *(v4i*)(lds_k + hi) = v4i{k2[0], k2[1], k3[0], k3[1]};
+            *(v4i*)(lds_v + lo) = v4i{v0[0], v0[1], v1[0], v1[1]};
+            *(v4i*)(lds_v + hi) = v4i{v2[0], v2[1], v3[0], v3[1]};
+        } else {
+            const int loff = key * S::ROW + ((ch ^ sw) << 4);
+            *(v4i*)(lds_k + loff) = kc;
+            *(v4i*)(lds_v + loff) = vc;
+        }
+    }
+}
+
+// Zero V rows [valid, 64) of a staged tile, so that masked (probability 0)
+// keys cannot inject NaN bit patterns from unused cache slots.
+template <class S>
+__device__ __forceinline__ void zero_masked_v(uint8_t* lds_v, int valid, int tid) {
+    for (int idx = tid; idx < (kKeyTile - valid) * S::CHUNKS; idx += kThreads)
+        *(v4i*)(lds_v + valid * S::ROW + idx * 16) = v4i{0, 0, 0, 0};
+}
+
+template <int D, bool STORE8, bool FP8>
+__global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_fwd_kernel(FwdArgs a) {
+    using S = TileShape<D, STORE8, FP8>;
+    constexpr int ROW = S::ROW, CHUNKS = S::CHUNKS, TILE = S::TILE, QK = S::QK, DT = S::DT;
+
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S::NBUF * 2 * TILE];
+
+    // ---- XCD-aware work mapping ------------------------------------------
+    // Workgroups are dealt to the 8 XCDs round-robin by launch index; give
+    // each XCD a contiguous range of (KV head, row tile) work items so that
+    // the workgroups sharing an XCD's L2 stream the same KV head together.
+    const int items = a.row_tiles * a.num_kv_heads;
+    const int per_xcd = (items + 7) / 8;
+    const int item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (item >= items) return;
+    const int head = item / a.row_tiles;
+    const int row_tile = item - head * a.row_tiles;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31;  // query column of the score tile / A-operand row
     const int h = lane >> 5;  // k-group (lane half)
-    const int head = blockIdx.y;
 
     // ---- this lane's query row -------------------------------------------
-    const int row = blockIdx.x * kRowsPerGroup + wave * kRowsPerWave + j;
+    const int row = row_tile * kRowsPerGroup + wave * kRowsPerWave + j;
     const bool row_ok = row < a.rows_per_head;
     const int rowc = row_ok ? row : a.rows_per_head - 1;
     const int rank = rowc / a.group_rows;
@@ -238,162 +386,152 @@ __global__ void __launch_bounds__(kThreads) history_fwd_kernel(FwdArgs a) {
     const int grp = lane >> 4;  // 16-lane group of the transposing reads
     const int gl = lane & 15;
 
-    for (int e = 0; e < a.num_entries; ++e) {
-        const int page = a.block_table[e];
-        const int n = min(a.page_valid_len[e], a.block_size);
-        if (n <= 0 || (unsigned)page >= (unsigned)a.num_pages) continue;
-        const uint8_t* const kpage = a.kv + (int64_t)page * a.page_stride + (int64_t)head * a.head_stride;
-        const uint8_t* const vpage = kpage + (int64_t)a.num_kv_heads * a.head_stride;
-
-        for (int base = 0; base < n; base += kKeyTile) {
-            const int valid = min(kKeyTile, n - base);
+    TileCursor cur = next_tile(a, head, TileCursor{-1, 0, 0, 0});
+    int buf = 0;
+    if constexpr (S::NBUF == 2) {
+        if (cur.e < a.num_entries) stage_tile_async<S>(a, cur, lds, lds + TILE, wave, lane);
+    }
+    while (cur.e < a.num_entries) {
+        const TileCursor nxt = next_tile(a, head, cur);
+        const int valid = min(kKeyTile, cur.n - cur.base);
+        uint8_t* const lds_k = lds + buf * 2 * TILE;
+        uint8_t* const lds_v = lds_k + TILE;
+        if constexpr (S::NBUF == 2) {
+            wait_vmem();      // this wave's loads of the current tile have landed
+            __syncthreads();  // ... and every wave's; the other buffer is free
+            if (nxt.e < a.num_entries)
+                stage_tile_async<S>(a, nxt, lds + (buf ^ 1) * 2 * TILE, lds + (buf ^ 1) * 2 * TILE + TILE, wave, lane);
+            if (valid < kKeyTile) {
+                zero_masked_v<S>(lds_v, valid, tid);
+                __syncthreads();
+            }
+        } else {
             __syncthreads();  // previous tile fully consumed
-#pragma unroll
-            for (int i = 0; i < LOADS; ++i) {
-                const int chunk_id = tid + kThreads * i;
-                const int key = chunk_id / GCHUNKS;
-                const int ch = chunk_id - key * GCHUNKS;
-                const int64_t goff = (int64_t)(base + key) * GROW + ch * 16;
-                const v4i kc = *(const v4i*)(kpage + goff);
-                v4i vc = *(const v4i*)(vpage + goff);
-                // Masked V rows are zeroed so that 0-probability keys cannot
-                // inject NaN/Inf bit patterns from unused cache slots.
-                if (key >= valid) vc = v4i{0, 0, 0, 0};
-                const int sw = chunk_swizzle<FP8, CHUNKS>(key);
-                if constexpr (WIDEN) {
-                    // 16 e4m3 codes become 32 bytes (LDS chunks 2ch, 2ch+1).
-                    const v2i k0 = e4m3x4_to_bf16x4(kc[0]), k1 = e4m3x4_to_bf16x4(kc[1]);
-                    const v2i k2 = e4m3x4_to_bf16x4(kc[2]), k3 = e4m3x4_to_bf16x4(kc[3]);
-                    const v2i v0 = e4m3x4_to_bf16x4(vc[0]), v1 = e4m3x4_to_bf16x4(vc[1]);
-                    const v2i v2 = e4m3x4_to_bf16x4(vc[2]), v3 = e4m3x4_to_bf16x4(vc[3]);
-                    const int lo = key * ROW + (((2 * ch) ^ sw) << 4);
-                    const int hi = key * ROW + (((2 * ch + 1) ^ sw) << 4);
-                    *(v4i*)(lds_k + lo) = v4i{k0[0], k0[1], k1[0], k1[1]};
-                    *(v4i*)(lds_k + hi) = v4i{k2[0], k2[1], k3[0], k3[1]};
-                    *(v4i*)(lds_v + lo) = v4i{v0[0], v0[1], v1[0], v1[1]};
-                    *(v4i*)(lds_v + hi) = v4i{v2[0], v2[1], v3[0], v3[1]};
-                } else {
-                    const int loff = key * ROW + ((ch ^ sw) << 4);
-                    *(v4i*)(lds_k + loff) = kc;
-                    *(v4i*)(lds_v + loff) = vc;
-                }
+            if constexpr (S::WIDEN) {
+                stage_tile_sync<S>(a, cur, valid, lds_k, lds_v, tid);
+            } else {
+                stage_tile_async<S>(a, cur, lds_k, lds_v, wave, lane);
+                wait_vmem();
+                __syncthreads();
+                if (valid < kKeyTile) zero_masked_v<S>(lds_v, valid, tid);
             }
             __syncthreads();
+        }
 
-            // ---- S^T = K . Q^T : two 32-key x 32-query tiles --------------
-            v16f s[2];
+        // ---- S^T = K . Q^T : two 32-key x 32-query tiles --------------
+        v16f s[2];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                s[t] = v16f{};
-                const uint8_t* const krow = lds_k + k_row_off[t];
+        for (int t = 0; t < 2; ++t) {
+            s[t] = v16f{};
+            const uint8_t* const krow = lds_k + k_row_off[t];
 #pragma unroll
-                for (int c = 0; c < QK; ++c) {
-                    if constexpr (FP8) {
-                        const v4i lo = *(const v4i*)(krow + (((4 * c + 2 * h) ^ k_swz[t]) << 4));
-                        const v4i hi = *(const v4i*)(krow + (((4 * c + 2 * h + 1) ^ k_swz[t]) << 4));
-                        const v8i aop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                        s[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, qop[c], s[t], 0, 0, 0, 0, 0, 0);
-                    } else {
-                        const v4i x = *(const v4i*)(krow + (((2 * c + h) ^ k_swz[t]) << 4));
-                        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, x), qop[c], s[t], 0, 0, 0);
-                    }
-                }
-            }
-
-            // ---- mask, online softmax ---------------------------------------
-            if (valid < kKeyTile) {
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        if (key_of_acc<FP8>(t, r, h) >= valid) s[t][r] = -INFINITY;
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
-            mx = halves_max(mx);
-            const float m_new = fmaxf(m_run, mx * cscale);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            float psum = 0.f;
-            const float shift = FP8 ? kPBiasLog2 - m_new : -m_new;
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], cscale, shift));
-                    s[t][r] = p;
-                    psum += p;
-                }
-            l_run = fmaf(l_run, alpha, psum);
-            m_run = m_new;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
-
-            // ---- O^T += V^T . P^T ---------------------------------------------
-            if constexpr (FP8) {
-                v8i pop;
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
-#pragma unroll
-                    for (int q4 = 0; q4 < 4; ++q4) {
-                        int pk = __builtin_amdgcn_cvt_pk_fp8_f32(s[t][4 * q4], s[t][4 * q4 + 1], 0, false);
-                        pk = __builtin_amdgcn_cvt_pk_fp8_f32(s[t][4 * q4 + 2], s[t][4 * q4 + 3], pk, true);
-                        pop[4 * t + q4] = pk;
-                    }
-                // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1): keys
-                // 32*(grp>>1) + [0, 32) of column d, 8 per transposing read.
-                const int vkey0 = 32 * (grp >> 1) + (gl >> 1);
-                const int vswz = chunk_swizzle<FP8, CHUNKS>(vkey0);  // same for vkey0 + 8*s
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    const int chunk = (2 * dt + (grp & 1)) ^ vswz;
-                    v8i aop;
-#pragma unroll
-                    for (int s4 = 0; s4 < 4; ++s4) {
-                        const int off = (vkey0 + 8 * s4) * ROW + (chunk << 4) + 8 * (gl & 1);
-                        const v2i x = __builtin_amdgcn_ds_read_tr8_b64_v2i32(PCPA_LDS(v2i, lds_v + off));
-                        aop[2 * s4] = x[0];
-                        aop[2 * s4 + 1] = x[1];
-                    }
-                    o[dt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, pop, o[dt], 0, 0, 0, 0, 0, 0);
-                }
-            } else {
-                v8bf pop[2][2];
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
-#pragma unroll
-                    for (int u = 0; u < 2; ++u)
-#pragma unroll
-                        for (int e2 = 0; e2 < 8; ++e2) pop[t][u][e2] = (__bf16)s[t][8 * u + e2];
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1).
-                    const int dbyte = 2 * (32 * dt + 16 * (grp & 1) + 4 * (gl & 3));
-#pragma unroll
-                    for (int t = 0; t < 2; ++t)
-#pragma unroll
-                        for (int u = 0; u < 2; ++u) {
-                            // Moved as whole dwords: element 4*s2 + b of the
-                            // operand is 16-bit half b of read s2.
-                            v4i aop;
-#pragma unroll
-                            for (int s2 = 0; s2 < 2; ++s2) {
-                                const int key = 32 * t + 16 * u + 8 * (grp >> 1) + 4 * s2 + (gl >> 2);
-                                const int off = key * ROW + (((dbyte >> 4) ^ chunk_swizzle<FP8, CHUNKS>(key)) << 4) +
-                                                (dbyte & 15);
-                                const v2i x = __builtin_bit_cast(
-                                    v2i, __builtin_amdgcn_ds_read_tr16_b64_v4i16(PCPA_LDS(v4s, lds_v + off)));
-                                aop[2 * s2] = x[0];
-                                aop[2 * s2 + 1] = x[1];
-                            }
-                            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop), pop[t][u],
-                                                                            o[dt], 0, 0, 0);
-                        }
+            for (int c = 0; c < QK; ++c) {
+                if constexpr (FP8) {
+                    const v4i lo = *(const v4i*)(krow + (((4 * c + 2 * h) ^ k_swz[t]) << 4));
+                    const v4i hi = *(const v4i*)(krow + (((4 * c + 2 * h + 1) ^ k_swz[t]) << 4));
+                    const v8i aop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    s[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, qop[c], s[t], 0, 0, 0, 0, 0, 0);
+                } else {
+                    const v4i x = *(const v4i*)(krow + (((2 * c + h) ^ k_swz[t]) << 4));
+                    s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, x), qop[c], s[t], 0, 0, 0);
                 }
             }
         }
+
+        // ---- mask, online softmax (lazy rescale) --------------------------
+        if (valid < kKeyTile) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (key_of_acc<FP8>(t, r, h) >= valid) s[t][r] = -INFINITY;
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+        const float mxs = halves_max(mx) * cscale;
+        if (__builtin_amdgcn_ballot_w64(mxs > m_run + S::RESCALE_LOG2) != 0) {
+            const float m_new = fmaxf(m_run, mxs);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+            m_run = m_new;
+        }
+        float psum = 0.f;
+        const float shift = (FP8 ? kPBiasLog2 : 0.f) - m_run;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], cscale, shift));
+                s[t][r] = p;
+                psum += p;
+            }
+        l_run += psum;
+
+        // ---- O^T += V^T . P^T ---------------------------------------------
+        if constexpr (FP8) {
+            v8i pop;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    int pk = __builtin_amdgcn_cvt_pk_fp8_f32(s[t][4 * q4], s[t][4 * q4 + 1], 0, false);
+                    pk = __builtin_amdgcn_cvt_pk_fp8_f32(s[t][4 * q4 + 2], s[t][4 * q4 + 3], pk, true);
+                    pop[4 * t + q4] = pk;
+                }
+            // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1): keys
+            // 32*(grp>>1) + [0, 32) of column d, 8 per transposing read.
+            const int vkey0 = 32 * (grp >> 1) + (gl >> 1);
+            const int vswz = chunk_swizzle<FP8, CHUNKS>(vkey0);  // same for vkey0 + 8*s
+            const uint32_t vbase = lds_address(lds_v) + vkey0 * ROW + 8 * (gl & 1);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const uint32_t addr = vbase + (((2 * dt + (grp & 1)) ^ vswz) << 4);
+                v2i x0 = ds_read_tr8_b64(addr), x1 = ds_read_tr8_b64(addr + 8 * ROW);
+                v2i x2 = ds_read_tr8_b64(addr + 16 * ROW), x3 = ds_read_tr8_b64(addr + 24 * ROW);
+                lds_results_ready(x0, x1, x2, x3);
+                const v8i aop = {x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
+                o[dt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, pop, o[dt], 0, 0, 0, 0, 0, 0);
+            }
+        } else {
+            v8bf pop[2][2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int e2 = 0; e2 < 8; ++e2) pop[t][u][e2] = (__bf16)s[t][8 * u + e2];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1).
+                const int dbyte = 2 * (32 * dt + 16 * (grp & 1) + 4 * (gl & 3));
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        // Moved as whole dwords: element 4*s2 + b of the
+                        // operand is 16-bit half b of read s2.
+                        v2i x[2];
+#pragma unroll
+                        for (int s2 = 0; s2 < 2; ++s2) {
+                            const int key = 32 * t + 16 * u + 8 * (grp >> 1) + 4 * s2 + (gl >> 2);
+                            const int off = key * ROW + (((dbyte >> 4) ^ chunk_swizzle<FP8, CHUNKS>(key)) << 4) +
+                                            (dbyte & 15);
+                            x[s2] = ds_read_tr16_b64(lds_address(lds_v + off));
+                        }
+                        lds_results_ready(x[0], x[1]);
+                        const v4i aop = {x[0][0], x[0][1], x[1][0], x[1][1]};
+                        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop), pop[t][u],
+                                                                        o[dt], 0, 0, 0);
+                    }
+            }
+        }
+        if constexpr (S::NBUF == 2) buf ^= 1;
+        cur = nxt;
     }
 
     // ---- epilogue: O = O^T / l, bf16 ---------------------------------------
@@ -501,7 +639,9 @@ int32_t pcpa_history_attention(const pcpa_params* p, const void* q, const void* 
     a.score_scale = p->softmax_scale * p->k_scale * pcpa::kLog2e;
     a.v_scale = p->v_scale;
 
-    const dim3 grid((a.rows_per_head + pcpa::kRowsPerGroup - 1) / pcpa::kRowsPerGroup, p->num_kv_heads);
+    a.row_tiles = (a.rows_per_head + pcpa::kRowsPerGroup - 1) / pcpa::kRowsPerGroup;
+    const int items = a.row_tiles * p->num_kv_heads;
+    const dim3 grid(8 * ((items + 7) / 8));
     const dim3 block(pcpa::kThreads);
     void* args[] = {&a};
     const void* fn = nullptr;

@@ -46,7 +46,25 @@ def parse_args(argv=None):
     parser.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
                         help="approximate CPU time budget of the ring-model baseline sample")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--traffic-bytes", type=float, default=None,
+                        help="HBM bytes per launch measured with rocprofv3 PMC counters (reported as roofline.traffic)")
+    parser.add_argument("--copy-probe-mib", type=int, default=0,
+                        help="instead of the benchmark, run --steps device-to-device copies of this many MiB "
+                             "(a known-size kernel for calibrating FETCH_SIZE / WRITE_SIZE)")
     return parser.parse_args(argv)
+
+
+def copy_probe(mib: int, steps: int) -> int:
+    import torch
+
+    device = torch.device("cuda", 0)
+    src = torch.ones(mib * (1 << 20), dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": src.numel(), "steps": steps}), flush=True)
+    return 0
 
 
 def model_flops(cfg) -> float:
@@ -112,6 +130,8 @@ def main(argv=None) -> int:
     if args.steps < 1 or args.warmup < 1:
         print("--steps and --warmup must be at least 1", file=sys.stderr)
         return 2
+    if args.copy_probe_mib:
+        return copy_probe(args.copy_probe_mib, args.steps)
 
     import torch
 
@@ -192,7 +212,7 @@ def main(argv=None) -> int:
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4),
-            "traffic": None,
+            "traffic": args.traffic_bytes,
             "algorithmic_bytes": algorithmic_bytes(cfg),
             "algorithmic_hbm_gbs": round(algorithmic_bytes(cfg) / (kernel_ms * 1e-3) / 1e9, 1),
         },
