@@ -112,11 +112,24 @@ __device__ __forceinline__ int key_of_row(int t, int rho) {
     return key_of_acc<FP8>(t, 4 * (rho >> 3) + (rho & 3), (rho >> 2) & 1);
 }
 
-// XOR swizzle of the 16-byte chunk index of LDS key row `key`.
+// LDS row holding key `key` of a 64-key tile.  FP8 tiles swap key bits 3
+// and 5: the 16 score-operand rows a 16-lane group reads (keys 32h+16t+r,
+// r < 8) and the 8 keys a transposing V read covers then differ in the low 4
+// row bits, and the per-lane part of every K, V and DMA address is the same
+// for all tiles t, reads s and DMA blocks.  BF16 tiles keep key order.
+template <bool FP8>
+__device__ __forceinline__ int lds_row(int key) {
+    if constexpr (FP8) return (key & ~0x28) | ((key >> 2) & 0x8) | ((key << 2) & 0x20);
+    return key;
+}
+
+// XOR swizzle of the 16-byte chunk index within LDS row `row`, making the
+// score-operand reads (16 rows per 16-lane group) and the transposing V
+// reads (8 rows x 16 bytes, or 4 rows x 32 bytes) bank-conflict free.
 template <bool FP8, int CHUNKS>
-__device__ __forceinline__ int chunk_swizzle(int key) {
+__device__ __forceinline__ int chunk_swizzle(int row) {
     constexpr int mask = (CHUNKS < 16 ? CHUNKS : 16) - 1;
-    const int s = FP8 ? ((key & 7) | (((key >> 5) & 1) << 3)) : (((key & 7) << 1) | ((key >> 3) & 1));
+    const int s = FP8 ? (row & 15) : (((row & 7) << 1) | ((row >> 3) & 1));
     return s & mask;
 }
 
@@ -137,28 +150,33 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // information, so the compiler orders them after every in-flight LDS DMA,
 // including the prefetch of the *other* buffer, which would serialise the
 // pipeline.  Ordering against this buffer's DMA is provided by the
-// vmcnt(0) + barrier at the top of each tile; the caller makes the results
-// usable with lds_results_ready().
+// vmcnt(0) + barrier at the top of each tile; lds_results_ready() makes the
+// results usable.  OFF is the instruction's immediate byte offset.
 __device__ __forceinline__ uint32_t lds_address(const uint8_t* p) {
     return (uint32_t)(uintptr_t)PCPA_LDS(const uint8_t, p);
 }
+template <int OFF>
 __device__ __forceinline__ v2i ds_read_tr8_b64(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
     v2i r;
-    asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(r) : "v"(addr));
+    asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
     return r;
 }
+template <int OFF>
 __device__ __forceinline__ v2i ds_read_tr16_b64(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
     v2i r;
-    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr));
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
     return r;
 }
 // s_waitcnt lgkmcnt(0), with the read results as operands so that no use of
-// them can be scheduled before the wait.
-__device__ __forceinline__ void lds_results_ready(v2i& a, v2i& b, v2i& c, v2i& d) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+// them (and no copy of the registers) can be scheduled before the wait.
+__device__ __forceinline__ void lds_results_ready(v2i (&x)[8]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7]));
 }
-__device__ __forceinline__ void lds_results_ready(v2i& a, v2i& b) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b));
+__device__ __forceinline__ void lds_results_ready(v2i (&x)[4]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]));
 }
 
 // Position in the walk over the block table: entry e (rank-major (rank,
@@ -195,6 +213,7 @@ template <int D, bool STORE8, bool FP8>
 struct TileShape {
     static_assert(STORE8 || !FP8, "e4m3 MFMAs need an e4m3 cache");
     static constexpr int ES = FP8 ? 1 : 2;
+    static constexpr bool F8 = FP8;
     static constexpr int ROW = D * ES;                 // LDS bytes of one key row
     static constexpr int CHUNKS = ROW / 16;
     static constexpr int TILE = kKeyTile * ROW;        // LDS bytes of one K (or V) tile
@@ -206,44 +225,63 @@ struct TileShape {
     static constexpr int NBUF = (!WIDEN && 4 * TILE <= 65536) ? 2 : 1;
     static constexpr int QK = FP8 ? D / 64 : D / 16;   // k-steps of the score MFMA
     static constexpr int DT = D / 32;                  // 32-row d tiles of O^T
+    static constexpr int DMA_PER_WAVE = CHUNKS / 4;    // 1 KB DMA blocks per wave per operand
+    // Wave w loads DMA blocks 4i + w.  Block i's lane chunk sits DMA_ROW_DELTA(i)
+    // key rows after block 0's, with the same chunk swizzle, except for 512-byte
+    // rows (bf16 D=256) whose swizzle changes between blocks: those keep one
+    // offset per block (DMA_SPLIT).
+    static constexpr bool DMA_SPLIT = ROW == 512;
+    static constexpr int K_T1_ROWS = FP8 ? 16 : 32;    // LDS rows from score tile 0 to tile 1
+    static constexpr int dma_key_delta(int i) {
+        // keys between DMA block i's lane chunk and block 0's (rows are 4i*1024/ROW apart)
+        return FP8 ? (ROW == 256 ? 16 * (i & 1) + 8 * (i >> 1) : ROW == 128 ? 8 * i : 0) : i * 4096 / ROW;
+    }
     // Lazy rescale: the running max is only raised when a tile's max exceeds
     // it by more than this (log2 units); FP8 probabilities then stay below
     // 2^(kPBiasLog2 + 2.5) = 362 < 448.
     static constexpr float RESCALE_LOG2 = FP8 ? 2.5f : 8.0f;
 };
 
-// Issue asynchronous global->LDS loads of one 64-key K tile and V tile.  The
-// tile is split into 1024-byte blocks; each wave loads CHUNKS/4 blocks of
-// each, one 16-byte chunk per lane, landing at block + 16 * lane.  The lane's
-// global chunk is chosen so that the swizzled LDS layout comes out.
+// Per-lane constants of the main loop (LDS offsets are within one buffer).
 template <class S>
-__device__ __forceinline__ void stage_tile_async(const FwdArgs& a, const TileCursor& c, uint8_t* lds_k,
-                                                 uint8_t* lds_v, int wave, int lane) {
-    constexpr int BLOCKS_PER_WAVE = S::CHUNKS / 4;
-    const uint8_t* const kpage = a.kv + c.k_off;
-    const uint8_t* const vpage = kpage + (int64_t)a.num_kv_heads * a.head_stride;
+struct LaneMap {
+    uint32_t k_addr;                      // score A operand of tile 0 (tile 1: + K_T1_ROWS rows)
+    uint32_t v_addr[S::ES == 1 ? 1 : 2];  // PV A operand base(s)
+    uint32_t dma_off[S::DMA_SPLIT ? S::DMA_PER_WAVE : 1];  // global byte offset of the lane's DMA chunk
+};
+
+// Issue asynchronous global->LDS loads of one 64-key K tile and V tile.  The
+// tile is split into 1 KB blocks; each wave loads DMA_PER_WAVE blocks of
+// each, one 16-byte chunk per lane, landing at block + 16 * lane.  The
+// lane's global chunk (dma_off) is chosen so that the swizzled LDS layout
+// comes out.
+template <class S, int BUF>
+__device__ __forceinline__ void stage_tile_async(const FwdArgs& a, const TileCursor& c, uint8_t* lds, int wave,
+                                                 const LaneMap<S>& L) {
+    const uint8_t* const kt = a.kv + c.k_off + (int64_t)c.base * S::GROW;
+    const uint8_t* const vt = kt + (int64_t)a.num_kv_heads * a.head_stride;
+    uint8_t* const lk = lds + BUF * 2 * S::TILE;
 #pragma unroll
-    for (int i = 0; i < BLOCKS_PER_WAVE; ++i) {
-        const int block = wave * BLOCKS_PER_WAVE + i;
-        const int byte = block * 1024 + lane * 16;
-        const int key = byte / S::ROW;
-        const int pos = (byte % S::ROW) / 16;
-        const int chunk = pos ^ chunk_swizzle<S::ES == 1, S::CHUNKS>(key);
-        const int64_t goff = (int64_t)(c.base + key) * S::GROW + chunk * 16;
-        __builtin_amdgcn_global_load_lds(kpage + goff, PCPA_LDS(void, lds_k + block * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vpage + goff, PCPA_LDS(void, lds_v + block * 1024), 16, 0, 0);
+    for (int i = 0; i < S::DMA_PER_WAVE; ++i) {
+        const int block = 4 * i + wave;
+        const uint32_t off = S::DMA_SPLIT ? L.dma_off[S::DMA_SPLIT ? i : 0] : L.dma_off[0];
+        const int delta = S::DMA_SPLIT ? 0 : S::dma_key_delta(i) * S::GROW;
+        __builtin_amdgcn_global_load_lds(kt + delta + off, PCPA_LDS(void, lk + block * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vt + delta + off, PCPA_LDS(void, lk + S::TILE + block * 1024), 16, 0, 0);
     }
 }
 
-// Synchronous staging through registers, widening e4m3 to bf16 when the
-// MFMAs are bf16.  Rows at or beyond `valid` get zero V.
+// Synchronous staging through registers into buffer 0, widening e4m3 to
+// bf16 when the MFMAs are bf16.  Rows at or beyond `valid` get zero V.
 template <class S>
-__device__ __forceinline__ void stage_tile_sync(const FwdArgs& a, const TileCursor& c, int valid, uint8_t* lds_k,
-                                                uint8_t* lds_v, int tid) {
+__device__ __forceinline__ void stage_tile_sync(const FwdArgs& a, const TileCursor& c, int valid, uint8_t* lds,
+                                                int tid) {
     constexpr int LOADS = kKeyTile * S::GROW / (16 * kThreads);
     static_assert((kKeyTile * S::GROW) % (16 * kThreads) == 0, "tile must split into 16-byte chunks per thread");
     const uint8_t* const kpage = a.kv + c.k_off;
     const uint8_t* const vpage = kpage + (int64_t)a.num_kv_heads * a.head_stride;
+    uint8_t* const lds_k = lds;
+    uint8_t* const lds_v = lds + S::TILE;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
         const int chunk_id = tid + kThreads * i;
@@ -253,21 +291,22 @@ __device__ __forceinline__ void stage_tile_sync(const FwdArgs& a, const TileCurs
         const v4i kc = *(const v4i*)(kpage + goff);
         v4i vc = *(const v4i*)(vpage + goff);
         if (key >= valid) vc = v4i{0, 0, 0, 0};
-        const int sw = chunk_swizzle<S::ES == 1, S::CHUNKS>(key);
+        const int row = lds_row<S::ES == 1>(key);
+        const int sw = chunk_swizzle<S::ES == 1, S::CHUNKS>(row);
         if constexpr (S::WIDEN) {
             // 16 e4m3 codes become 32 bytes (LDS chunks 2ch, 2ch+1).
             const v2i k0 = e4m3x4_to_bf16x4(kc[0]), k1 = e4m3x4_to_bf16x4(kc[1]);
             const v2i k2 = e4m3x4_to_bf16x4(kc[2]), k3 = e4m3x4_to_bf16x4(kc[3]);
             const v2i v0 = e4m3x4_to_bf16x4(vc[0]), v1 = e4m3x4_to_bf16x4(vc[1]);
             const v2i v2 = e4m3x4_to_bf16x4(vc[2]), v3 = e4m3x4_to_bf16x4(vc[3]);
-            const int lo = key * S::ROW + (((2 * ch) ^ sw) << 4);
-            const int hi = key * S::ROW + (((2 * ch + 1) ^ sw) << 4);
+            const int lo = row * S::ROW + (((2 * ch) ^ sw) << 4);
+            const int hi = row * S::ROW + (((2 * ch + 1) ^ sw) << 4);
             *(v4i*)(lds_k + lo) = v4i{k0[0], k0[1], k1[0], k1[1]};
             *(v4i*)(lds_k + hi) = v4i{k2[0], k2[1], k3[0], k3[1]};
             *(v4i*)(lds_v + lo) = v4i{v0[0], v0[1], v1[0], v1[1]};
             *(v4i*)(lds_v + hi) = v4i{v2[0], v2[1], v3[0], v3[1]};
         } else {
-            const int loff = key * S::ROW + ((ch ^ sw) << 4);
+            const int loff = row * S::ROW + ((ch ^ sw) << 4);
             *(v4i*)(lds_k + loff) = kc;
             *(v4i*)(lds_v + loff) = vc;
         }
@@ -278,16 +317,210 @@ __device__ __forceinline__ void stage_tile_sync(const FwdArgs& a, const TileCurs
 // keys cannot inject NaN bit patterns from unused cache slots.
 template <class S>
 __device__ __forceinline__ void zero_masked_v(uint8_t* lds_v, int valid, int tid) {
-    for (int idx = tid; idx < (kKeyTile - valid) * S::CHUNKS; idx += kThreads)
-        *(v4i*)(lds_v + valid * S::ROW + idx * 16) = v4i{0, 0, 0, 0};
+    for (int idx = tid; idx < (kKeyTile - valid) * S::CHUNKS; idx += kThreads) {
+        const int key = valid + idx / S::CHUNKS;
+        *(v4i*)(lds_v + lds_row<S::ES == 1>(key) * S::ROW + (idx % S::CHUNKS) * 16) = v4i{0, 0, 0, 0};
+    }
+}
+
+// Online-softmax state of one lane: running max (log2 domain, times the
+// lane's score factor), this lane half's share of the running sum, and the
+// O^T accumulator tiles.
+template <class S>
+struct SoftmaxState {
+    float m;
+    float l;
+    v16f o[S::DT];
+};
+
+template <class S>
+using QOperand = typename std::conditional<S::ES == 1, v8i, v8bf>::type;
+
+// One 64-key tile held in LDS buffer BUF: S^T = K Q^T, masked online
+// softmax, O^T += V^T P^T.
+template <class S, int BUF>
+__device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, const QOperand<S> (&qop)[S::QK],
+                                             float cscale, const LaneMap<S>& L, int h, SoftmaxState<S>& st) {
+    constexpr bool FP8 = S::ES == 1;
+    constexpr int ROW = S::ROW, QK = S::QK, DT = S::DT;
+    constexpr int KBASE = BUF * 2 * S::TILE;
+    constexpr int VBASE = KBASE + S::TILE;
+    const uint8_t* const lk = lds + KBASE;
+
+    // ---- S^T = K . Q^T : two 32-key x 32-query tiles --------------------
+    v16f s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        s[t] = v16f{};
+#pragma unroll
+        for (int c = 0; c < QK; ++c) {
+            const uint8_t* const kt = lk + t * S::K_T1_ROWS * ROW;
+            if constexpr (FP8) {
+                const v4i lo = *(const v4i*)(kt + (L.k_addr ^ ((4 * c) << 4)));
+                const v4i hi = *(const v4i*)(kt + (L.k_addr ^ ((4 * c + 1) << 4)));
+                const v8i aop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                s[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, qop[c], s[t], 0, 0, 0, 0, 0, 0);
+            } else {
+                const v4i x = *(const v4i*)(kt + (L.k_addr ^ ((2 * c) << 4)));
+                s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, x), qop[c], s[t], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- mask, online softmax (lazy rescale) ----------------------------
+    if (valid < kKeyTile) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (key_of_acc<FP8>(t, r, h) >= valid) s[t][r] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+    const float mxs = halves_max(mx) * cscale;
+    if (__builtin_amdgcn_ballot_w64(mxs > st.m + S::RESCALE_LOG2) != 0) {
+        const float m_new = fmaxf(st.m, mxs);
+        const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+        st.l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) st.o[dt] *= alpha;
+        st.m = m_new;
+    }
+    float psum = 0.f;
+    const float shift = (FP8 ? kPBiasLog2 : 0.f) - st.m;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], cscale, shift));
+            s[t][r] = p;
+            psum += p;
+        }
+    st.l += psum;
+
+    // ---- O^T += V^T . P^T -----------------------------------------------
+    if constexpr (FP8) {
+        v8i pop;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                // The first convert's untouched high half is overwritten by
+                // the second, so any register serves as its "old" operand.
+                int pk = __builtin_amdgcn_cvt_pk_fp8_f32(s[t][4 * q4], s[t][4 * q4 + 1],
+                                                         __float_as_int(s[t][4 * q4]), false);
+                pk = __builtin_amdgcn_cvt_pk_fp8_f32(s[t][4 * q4 + 2], s[t][4 * q4 + 3], pk, true);
+                pop[4 * t + q4] = pk;
+            }
+        // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1): keys
+        // 32*(grp>>1) + [0, 32) of column d, 8 per transposing read; the
+        // d tiles are read two at a time, one pair ahead of the MFMAs.
+        constexpr int PAIRS = DT / 2;
+        v2i x[2][8];
+        auto issue = [&](v2i (&buf)[8], int pair) {
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t addr = L.v_addr[0] ^ ((2 * (2 * pair + k)) << 4);
+                // keys 32g + 8s + m live in LDS rows (8g + m) + {0, 32, 16, 48}[s]
+                buf[4 * k + 0] = ds_read_tr8_b64<VBASE + 0 * ROW>(addr);
+                buf[4 * k + 1] = ds_read_tr8_b64<VBASE + 32 * ROW>(addr);
+                buf[4 * k + 2] = ds_read_tr8_b64<VBASE + 16 * ROW>(addr);
+                buf[4 * k + 3] = ds_read_tr8_b64<VBASE + 48 * ROW>(addr);
+            }
+        };
+        issue(x[0], 0);
+#pragma unroll
+        for (int pair = 0; pair < PAIRS; ++pair) {
+            v2i(&cur)[8] = x[pair & 1];
+            lds_results_ready(cur);
+            if (pair + 1 < PAIRS) issue(x[(pair + 1) & 1], pair + 1);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const v8i aop = {cur[4 * k][0],     cur[4 * k][1],     cur[4 * k + 1][0], cur[4 * k + 1][1],
+                                 cur[4 * k + 2][0], cur[4 * k + 2][1], cur[4 * k + 3][0], cur[4 * k + 3][1]};
+                st.o[2 * pair + k] =
+                    __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, pop, st.o[2 * pair + k], 0, 0, 0, 0, 0, 0);
+            }
+        }
+    } else {
+        v8bf pop[2][2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int e2 = 0; e2 < 8; ++e2) pop[t][u][e2] = (__bf16)s[t][8 * u + e2];
+        // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1): for score
+        // tile t and half u, keys 32t + 16u + 8*(grp>>1) + [0, 8) of column
+        // d, 4 per transposing read.
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const uint32_t a0 = L.v_addr[0] ^ ((4 * dt) << 4);
+            const uint32_t a1 = L.v_addr[1] ^ ((4 * dt) << 4);
+            v2i x[4];
+            x[0] = ds_read_tr16_b64<VBASE>(a0);
+            x[1] = ds_read_tr16_b64<VBASE>(a1);
+            x[2] = ds_read_tr16_b64<VBASE + 16 * ROW>(a0);
+            x[3] = ds_read_tr16_b64<VBASE + 16 * ROW>(a1);
+            lds_results_ready(x);
+            const v4i aop0 = {x[0][0], x[0][1], x[1][0], x[1][1]};
+            const v4i aop1 = {x[2][0], x[2][1], x[3][0], x[3][1]};
+            st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop0), pop[0][0], st.o[dt], 0, 0, 0);
+            st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop1), pop[0][1], st.o[dt], 0, 0, 0);
+            v2i y[4];
+            y[0] = ds_read_tr16_b64<VBASE + 32 * ROW>(a0);
+            y[1] = ds_read_tr16_b64<VBASE + 32 * ROW>(a1);
+            y[2] = ds_read_tr16_b64<VBASE + 48 * ROW>(a0);
+            y[3] = ds_read_tr16_b64<VBASE + 48 * ROW>(a1);
+            lds_results_ready(y);
+            const v4i aop2 = {y[0][0], y[0][1], y[1][0], y[1][1]};
+            const v4i aop3 = {y[2][0], y[2][1], y[3][0], y[3][1]};
+            st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop2), pop[1][0], st.o[dt], 0, 0, 0);
+            st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop3), pop[1][1], st.o[dt], 0, 0, 0);
+        }
+    }
+}
+
+// Wait for tile `cur` (in BUF), start the prefetch of `nxt` into the other
+// buffer, then compute `cur`.
+template <class S, int BUF>
+__device__ __forceinline__ void tile_step(const FwdArgs& a, const TileCursor& cur, const TileCursor& nxt,
+                                          uint8_t* lds, int wave, int tid, int h, const LaneMap<S>& L,
+                                          const QOperand<S> (&qop)[S::QK], float cscale, SoftmaxState<S>& st) {
+    const int valid = min(kKeyTile, cur.n - cur.base);
+    uint8_t* const lds_v = lds + BUF * 2 * S::TILE + S::TILE;
+    if constexpr (S::NBUF == 2) {
+        wait_vmem();      // this wave's loads of the current tile have landed
+        __syncthreads();  // ... and every wave's; the other buffer is free
+        if (nxt.e < a.num_entries) stage_tile_async<S, BUF ^ 1>(a, nxt, lds, wave, L);
+        if (valid < kKeyTile) {
+            zero_masked_v<S>(lds_v, valid, tid);
+            __syncthreads();
+        }
+    } else {
+        __syncthreads();  // previous tile fully consumed
+        if constexpr (S::WIDEN) {
+            stage_tile_sync<S>(a, cur, valid, lds, tid);
+        } else {
+            stage_tile_async<S, 0>(a, cur, lds, wave, L);
+            wait_vmem();
+            __syncthreads();
+            if (valid < kKeyTile) zero_masked_v<S>(lds_v, valid, tid);
+        }
+        __syncthreads();
+    }
+    compute_tile<S, BUF>(lds, valid, qop, cscale, L, h, st);
 }
 
 template <int D, bool STORE8, bool FP8>
 __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_fwd_kernel(FwdArgs a) {
     using S = TileShape<D, STORE8, FP8>;
-    constexpr int ROW = S::ROW, CHUNKS = S::CHUNKS, TILE = S::TILE, QK = S::QK, DT = S::DT;
+    constexpr int ROW = S::ROW, CHUNKS = S::CHUNKS, QK = S::QK, DT = S::DT;
 
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[S::NBUF * 2 * TILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S::NBUF * 2 * S::TILE];
 
     // ---- XCD-aware work mapping ------------------------------------------
     // Workgroups are dealt to the 8 XCDs round-robin by launch index; give
@@ -305,6 +538,8 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31;  // query column of the score tile / A-operand row
     const int h = lane >> 5;  // k-group (lane half)
+    const int grp = lane >> 4;
+    const int gl = lane & 15;
 
     // ---- this lane's query row -------------------------------------------
     const int row = row_tile * kRowsPerGroup + wave * kRowsPerWave + j;
@@ -319,8 +554,7 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
     const uint8_t* const qrow = a.q + row_off;
 
     // ---- Q^T operand (register resident for the whole history) ------------
-    using QOp = typename std::conditional<FP8, v8i, v8bf>::type;
-    QOp qop[QK];
+    QOperand<S> qop[QK];
     float cscale;
     if constexpr (FP8) {
         // lane (j, h) holds d = 64c + 32h + [0, 32) of its row, as e4m3.
@@ -368,174 +602,60 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
         cscale = a.score_scale;
     }
 
-    // ---- online softmax state ---------------------------------------------
-    float m_run = -INFINITY;  // running max of score * cscale (log2 domain)
-    float l_run = 0.f;        // this lane half's share of the running sum
-    v16f o[DT];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] = v16f{};
-
-    // Per-lane LDS read offsets that do not depend on the tile.
-    int k_row_off[2], k_swz[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int key = key_of_row<FP8>(t, j);
-        k_row_off[t] = key * ROW;
-        k_swz[t] = chunk_swizzle<FP8, CHUNKS>(key);
+    // ---- per-lane LDS / DMA offsets ---------------------------------------
+    // Row offsets are multiples of ROW (a power of two) and the chunk field
+    // lies below ROW, so XOR-ing a constant into the chunk field is one v_xor.
+    LaneMap<S> L;
+    {
+        const int row = lds_row<FP8>(key_of_row<FP8>(0, j));
+        const int first_chunk = FP8 ? 2 * h : h;
+        L.k_addr = row * ROW + ((first_chunk ^ chunk_swizzle<FP8, CHUNKS>(row)) << 4);
     }
-    const int grp = lane >> 4;  // 16-lane group of the transposing reads
-    const int gl = lane & 15;
+    if constexpr (FP8) {
+        // key 32*(grp>>1) + (gl>>1) (+ 8s for the other reads) -> row below
+        const int row = lds_row<FP8>(32 * (grp >> 1) + (gl >> 1));
+        L.v_addr[0] = row * ROW + (((grp & 1) ^ chunk_swizzle<FP8, CHUNKS>(row)) << 4) + 8 * (gl & 1);
+    } else {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const int vkey = 8 * (grp >> 1) + 4 * s2 + (gl >> 2);  // + 16u + 32t: same swizzle
+            const int dbyte = 2 * (16 * (grp & 1) + 4 * (gl & 3));
+            L.v_addr[s2] = vkey * ROW + (((dbyte >> 4) ^ chunk_swizzle<FP8, CHUNKS>(vkey)) << 4) + (dbyte & 15);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < (S::DMA_SPLIT ? S::DMA_PER_WAVE : 1); ++i) {
+        const int byte = (4 * i + wave) * 1024 + lane * 16;
+        const int row = byte / ROW;
+        const int chunk = ((byte % ROW) / 16) ^ chunk_swizzle<FP8, CHUNKS>(row);
+        L.dma_off[i] = lds_row<FP8>(row) * S::GROW + chunk * 16;
+    }
+
+    // ---- walk the block table -----------------------------------------------
+    SoftmaxState<S> st;
+    st.m = -INFINITY;
+    st.l = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) st.o[dt] = v16f{};
 
     TileCursor cur = next_tile(a, head, TileCursor{-1, 0, 0, 0});
-    int buf = 0;
     if constexpr (S::NBUF == 2) {
-        if (cur.e < a.num_entries) stage_tile_async<S>(a, cur, lds, lds + TILE, wave, lane);
+        if (cur.e < a.num_entries) stage_tile_async<S, 0>(a, cur, lds, wave, L);
     }
     while (cur.e < a.num_entries) {
-        const TileCursor nxt = next_tile(a, head, cur);
-        const int valid = min(kKeyTile, cur.n - cur.base);
-        uint8_t* const lds_k = lds + buf * 2 * TILE;
-        uint8_t* const lds_v = lds_k + TILE;
-        if constexpr (S::NBUF == 2) {
-            wait_vmem();      // this wave's loads of the current tile have landed
-            __syncthreads();  // ... and every wave's; the other buffer is free
-            if (nxt.e < a.num_entries)
-                stage_tile_async<S>(a, nxt, lds + (buf ^ 1) * 2 * TILE, lds + (buf ^ 1) * 2 * TILE + TILE, wave, lane);
-            if (valid < kKeyTile) {
-                zero_masked_v<S>(lds_v, valid, tid);
-                __syncthreads();
-            }
-        } else {
-            __syncthreads();  // previous tile fully consumed
-            if constexpr (S::WIDEN) {
-                stage_tile_sync<S>(a, cur, valid, lds_k, lds_v, tid);
-            } else {
-                stage_tile_async<S>(a, cur, lds_k, lds_v, wave, lane);
-                wait_vmem();
-                __syncthreads();
-                if (valid < kKeyTile) zero_masked_v<S>(lds_v, valid, tid);
-            }
-            __syncthreads();
-        }
-
-        // ---- S^T = K . Q^T : two 32-key x 32-query tiles --------------
-        v16f s[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            s[t] = v16f{};
-            const uint8_t* const krow = lds_k + k_row_off[t];
-#pragma unroll
-            for (int c = 0; c < QK; ++c) {
-                if constexpr (FP8) {
-                    const v4i lo = *(const v4i*)(krow + (((4 * c + 2 * h) ^ k_swz[t]) << 4));
-                    const v4i hi = *(const v4i*)(krow + (((4 * c + 2 * h + 1) ^ k_swz[t]) << 4));
-                    const v8i aop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    s[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, qop[c], s[t], 0, 0, 0, 0, 0, 0);
-                } else {
-                    const v4i x = *(const v4i*)(krow + (((2 * c + h) ^ k_swz[t]) << 4));
-                    s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, x), qop[c], s[t], 0, 0, 0);
-                }
-            }
-        }
-
-        // ---- mask, online softmax (lazy rescale) --------------------------
-        if (valid < kKeyTile) {
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (key_of_acc<FP8>(t, r, h) >= valid) s[t][r] = -INFINITY;
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
-        const float mxs = halves_max(mx) * cscale;
-        if (__builtin_amdgcn_ballot_w64(mxs > m_run + S::RESCALE_LOG2) != 0) {
-            const float m_new = fmaxf(m_run, mxs);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            l_run *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
-            m_run = m_new;
-        }
-        float psum = 0.f;
-        const float shift = (FP8 ? kPBiasLog2 : 0.f) - m_run;
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], cscale, shift));
-                s[t][r] = p;
-                psum += p;
-            }
-        l_run += psum;
-
-        // ---- O^T += V^T . P^T ---------------------------------------------
-        if constexpr (FP8) {
-            v8i pop;
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4) {
-                    int pk = __builtin_amdgcn_cvt_pk_fp8_f32(s[t][4 * q4], s[t][4 * q4 + 1], 0, false);
-                    pk = __builtin_amdgcn_cvt_pk_fp8_f32(s[t][4 * q4 + 2], s[t][4 * q4 + 3], pk, true);
-                    pop[4 * t + q4] = pk;
-                }
-            // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1): keys
-            // 32*(grp>>1) + [0, 32) of column d, 8 per transposing read.
-            const int vkey0 = 32 * (grp >> 1) + (gl >> 1);
-            const int vswz = chunk_swizzle<FP8, CHUNKS>(vkey0);  // same for vkey0 + 8*s
-            const uint32_t vbase = lds_address(lds_v) + vkey0 * ROW + 8 * (gl & 1);
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                const uint32_t addr = vbase + (((2 * dt + (grp & 1)) ^ vswz) << 4);
-                v2i x0 = ds_read_tr8_b64(addr), x1 = ds_read_tr8_b64(addr + 8 * ROW);
-                v2i x2 = ds_read_tr8_b64(addr + 16 * ROW), x3 = ds_read_tr8_b64(addr + 24 * ROW);
-                lds_results_ready(x0, x1, x2, x3);
-                const v8i aop = {x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
-                o[dt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, pop, o[dt], 0, 0, 0, 0, 0, 0);
-            }
-        } else {
-            v8bf pop[2][2];
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int u = 0; u < 2; ++u)
-#pragma unroll
-                    for (int e2 = 0; e2 < 8; ++e2) pop[t][u][e2] = (__bf16)s[t][8 * u + e2];
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1).
-                const int dbyte = 2 * (32 * dt + 16 * (grp & 1) + 4 * (gl & 3));
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
-#pragma unroll
-                    for (int u = 0; u < 2; ++u) {
-                        // Moved as whole dwords: element 4*s2 + b of the
-                        // operand is 16-bit half b of read s2.
-                        v2i x[2];
-#pragma unroll
-                        for (int s2 = 0; s2 < 2; ++s2) {
-                            const int key = 32 * t + 16 * u + 8 * (grp >> 1) + 4 * s2 + (gl >> 2);
-                            const int off = key * ROW + (((dbyte >> 4) ^ chunk_swizzle<FP8, CHUNKS>(key)) << 4) +
-                                            (dbyte & 15);
-                            x[s2] = ds_read_tr16_b64(lds_address(lds_v + off));
-                        }
-                        lds_results_ready(x[0], x[1]);
-                        const v4i aop = {x[0][0], x[0][1], x[1][0], x[1][1]};
-                        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop), pop[t][u],
-                                                                        o[dt], 0, 0, 0);
-                    }
-            }
-        }
-        if constexpr (S::NBUF == 2) buf ^= 1;
+        TileCursor nxt = next_tile(a, head, cur);
+        tile_step<S, 0>(a, cur, nxt, lds, wave, tid, h, L, qop, cscale, st);
         cur = nxt;
+        if constexpr (S::NBUF == 2) {
+            if (cur.e >= a.num_entries) break;
+            nxt = next_tile(a, head, cur);
+            tile_step<S, 1>(a, cur, nxt, lds, wave, tid, h, L, qop, cscale, st);
+            cur = nxt;
+        }
     }
 
     // ---- epilogue: O = O^T / l, bf16 ---------------------------------------
-    const float l_tot = halves_sum(l_run);
+    const float l_tot = halves_sum(st.l);
     const float scale = l_tot > 0.f ? a.v_scale / l_tot : 0.f;
     if (row_ok) {
         uint8_t* const orow = a.out + row_off;
@@ -544,10 +664,10 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
                 const int d = 32 * dt + 8 * r4 + 4 * h;
-                __bf16 v0 = (__bf16)(o[dt][4 * r4 + 0] * scale);
-                __bf16 v1 = (__bf16)(o[dt][4 * r4 + 1] * scale);
-                __bf16 v2 = (__bf16)(o[dt][4 * r4 + 2] * scale);
-                __bf16 v3 = (__bf16)(o[dt][4 * r4 + 3] * scale);
+                __bf16 v0 = (__bf16)(st.o[dt][4 * r4 + 0] * scale);
+                __bf16 v1 = (__bf16)(st.o[dt][4 * r4 + 1] * scale);
+                __bf16 v2 = (__bf16)(st.o[dt][4 * r4 + 2] * scale);
+                __bf16 v3 = (__bf16)(st.o[dt][4 * r4 + 3] * scale);
                 const uint32_t w0 = (uint32_t)__builtin_bit_cast(uint16_t, v0) |
                                     ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16);
                 const uint32_t w1 = (uint32_t)__builtin_bit_cast(uint16_t, v2) |
