@@ -132,6 +132,15 @@ __device__ __forceinline__ int chunk_swizzle(int row) {
     const int s = FP8 ? (row & 15) : (((row & 7) << 1) | ((row >> 3) & 1));
     return s & mask;
 }
+// FP8 V tiles use an even-only swizzle: the two 16-lane groups of a
+// transposing read that share rows (d halves 2dt and 2dt+1) then land on
+// disjoint chunk sets (even vs odd), so 32 lanes cover all 64 banks once.
+template <bool FP8, int CHUNKS>
+__device__ __forceinline__ int chunk_swizzle_v(int row) {
+    constexpr int mask = (CHUNKS < 16 ? CHUNKS : 16) - 1;
+    if constexpr (FP8) return (2 * row) & mask & 14;
+    return chunk_swizzle<FP8, CHUNKS>(row);
+}
 
 // Four bf16 values (8 bytes) widened exactly from four e4m3 codes (one dword).
 __device__ __forceinline__ v2i e4m3x4_to_bf16x4(int codes) {
@@ -247,7 +256,8 @@ template <class S>
 struct LaneMap {
     uint32_t k_addr;                      // score A operand of tile 0 (tile 1: + K_T1_ROWS rows)
     uint32_t v_addr[S::ES == 1 ? 1 : 2];  // PV A operand base(s)
-    uint32_t dma_off[S::DMA_SPLIT ? S::DMA_PER_WAVE : 1];  // global byte offset of the lane's DMA chunk
+    uint32_t dma_off[S::DMA_SPLIT ? S::DMA_PER_WAVE : 1];   // global byte offset of the lane's K DMA chunk
+    uint32_t dma_off_v[S::DMA_SPLIT ? S::DMA_PER_WAVE : 1]; // same for the V tile (its own swizzle)
 };
 
 // Issue asynchronous global->LDS loads of one 64-key K tile and V tile.  The
@@ -264,10 +274,11 @@ __device__ __forceinline__ void stage_tile_async(const FwdArgs& a, const TileCur
 #pragma unroll
     for (int i = 0; i < S::DMA_PER_WAVE; ++i) {
         const int block = 4 * i + wave;
-        const uint32_t off = S::DMA_SPLIT ? L.dma_off[S::DMA_SPLIT ? i : 0] : L.dma_off[0];
+        const uint32_t koff = L.dma_off[S::DMA_SPLIT ? i : 0];
+        const uint32_t voff = L.dma_off_v[S::DMA_SPLIT ? i : 0];
         const int delta = S::DMA_SPLIT ? 0 : S::dma_key_delta(i) * S::GROW;
-        __builtin_amdgcn_global_load_lds(kt + delta + off, PCPA_LDS(void, lk + block * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vt + delta + off, PCPA_LDS(void, lk + S::TILE + block * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(kt + delta + koff, PCPA_LDS(void, lk + block * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vt + delta + voff, PCPA_LDS(void, lk + S::TILE + block * 1024), 16, 0, 0);
     }
 }
 
@@ -293,6 +304,7 @@ __device__ __forceinline__ void stage_tile_sync(const FwdArgs& a, const TileCurs
         if (key >= valid) vc = v4i{0, 0, 0, 0};
         const int row = lds_row<S::ES == 1>(key);
         const int sw = chunk_swizzle<S::ES == 1, S::CHUNKS>(row);
+        const int swv = chunk_swizzle_v<S::ES == 1, S::CHUNKS>(row);
         if constexpr (S::WIDEN) {
             // 16 e4m3 codes become 32 bytes (LDS chunks 2ch, 2ch+1).
             const v2i k0 = e4m3x4_to_bf16x4(kc[0]), k1 = e4m3x4_to_bf16x4(kc[1]);
@@ -306,9 +318,8 @@ __device__ __forceinline__ void stage_tile_sync(const FwdArgs& a, const TileCurs
             *(v4i*)(lds_v + lo) = v4i{v0[0], v0[1], v1[0], v1[1]};
             *(v4i*)(lds_v + hi) = v4i{v2[0], v2[1], v3[0], v3[1]};
         } else {
-            const int loff = row * S::ROW + ((ch ^ sw) << 4);
-            *(v4i*)(lds_k + loff) = kc;
-            *(v4i*)(lds_v + loff) = vc;
+            *(v4i*)(lds_k + row * S::ROW + ((ch ^ sw) << 4)) = kc;
+            *(v4i*)(lds_v + row * S::ROW + ((ch ^ swv) << 4)) = vc;
         }
     }
 }
@@ -614,7 +625,7 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
     if constexpr (FP8) {
         // key 32*(grp>>1) + (gl>>1) (+ 8s for the other reads) -> row below
         const int row = lds_row<FP8>(32 * (grp >> 1) + (gl >> 1));
-        L.v_addr[0] = row * ROW + (((grp & 1) ^ chunk_swizzle<FP8, CHUNKS>(row)) << 4) + 8 * (gl & 1);
+        L.v_addr[0] = row * ROW + (((grp & 1) ^ chunk_swizzle_v<FP8, CHUNKS>(row)) << 4) + 8 * (gl & 1);
     } else {
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
@@ -627,8 +638,9 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
     for (int i = 0; i < (S::DMA_SPLIT ? S::DMA_PER_WAVE : 1); ++i) {
         const int byte = (4 * i + wave) * 1024 + lane * 16;
         const int row = byte / ROW;
-        const int chunk = ((byte % ROW) / 16) ^ chunk_swizzle<FP8, CHUNKS>(row);
-        L.dma_off[i] = lds_row<FP8>(row) * S::GROW + chunk * 16;
+        const int pos = (byte % ROW) / 16;
+        L.dma_off[i] = lds_row<FP8>(row) * S::GROW + (pos ^ chunk_swizzle<FP8, CHUNKS>(row)) * 16;
+        L.dma_off_v[i] = lds_row<FP8>(row) * S::GROW + (pos ^ chunk_swizzle_v<FP8, CHUNKS>(row)) * 16;
     }
 
     // ---- walk the block table -----------------------------------------------
