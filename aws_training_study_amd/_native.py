@@ -35,6 +35,7 @@ DTYPE_BF16 = 1
 DTYPE_FP8_E4M3FN = 2
 
 FLAG_BF16_MFMA = 1
+FLAG_EXACT_EXP2 = 2
 
 # Every symbol the header declares; the CPU test suite checks they resolve.
 EXPORTED_SYMBOLS = (

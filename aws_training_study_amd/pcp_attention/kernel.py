@@ -46,6 +46,7 @@ def pack_local_kv(k: Any, v: Any) -> Any:
 _KV_DTYPE_CODES = {"fp8_e4m3fn": 2, "bfloat16": 1}
 
 PRECISIONS = ("auto", "fp8", "bf16")
+EXP2_MODES = ("fast", "exact")
 # Below this many valid history tokens, ``precision="auto"`` runs an e4m3
 # cache through BF16 MFMAs: e4m3 rounding of Q and P is noise that is only
 # averaged away over many keys (at 785 tokens it reaches a 2e-2 max error).
@@ -78,6 +79,12 @@ class HistoryAttentionKernel:
       MFMAs (Q and P rounded to e4m3), ``"bf16"`` as BF16 MFMAs on the exactly
       widened cache, and ``"auto"`` picks ``"bf16"`` when the config's
       ``actual_history_len`` is below ``AUTO_BF16_BELOW_TOKENS``.
+    * ``exp2``: how the e4m3 MFMA path at head_dim 256 forms the e4m3
+      probabilities.  ``"fast"`` (default) writes the e4m3 code of 2^x
+      directly, interpolating the exponential linearly between powers of two
+      (at most 6.1% high before the e4m3 rounding, a +-3% shape error after
+      normalisation); ``"exact"`` rounds ``v_exp_f32``.  Other paths always
+      use ``v_exp_f32``.
 
     The launch is asynchronous on the current torch stream.
     """
@@ -141,12 +148,15 @@ class HistoryAttentionKernel:
         v_scale: float = 1.0,
         out=None,
         precision: str = "auto",
+        exp2: str = "fast",
     ):
         import torch
 
         cfg = self.config
         if precision not in PRECISIONS:
             raise ValueError(f"precision must be one of {PRECISIONS}, got {precision!r}")
+        if exp2 not in EXP2_MODES:
+            raise ValueError(f"exp2 must be one of {EXP2_MODES}, got {exp2!r}")
         if not q.is_cuda:
             raise ValueError("q must be a GPU tensor")
         device = q.device
@@ -188,7 +198,9 @@ class HistoryAttentionKernel:
             raise ValueError(f"out must be contiguous bfloat16 {q_shape} on {device}")
         params = self._params(num_pages, k_scale, v_scale)
         if self.uses_bf16_mfma(precision):
-            params.flags = self._native.FLAG_BF16_MFMA
+            params.flags |= self._native.FLAG_BF16_MFMA
+        if exp2 == "exact":
+            params.flags |= self._native.FLAG_EXACT_EXP2
         with torch.cuda.device(device):
             stream = torch.cuda.current_stream(device).cuda_stream
             status = self._lib.pcpa_history_attention(

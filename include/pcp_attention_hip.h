@@ -47,6 +47,12 @@ extern "C" {
  * e4m3 rounding of Q and P (which matters for short histories, where that
  * noise is not averaged over many keys).  Ignored for a bf16 cache. */
 #define PCPA_FLAG_BF16_MFMA 1u
+/* FP8 MFMA path at head_dim 256: compute the e4m3 probabilities with
+ * v_exp_f32 instead of the default linear-mantissa exp2 (which writes the
+ * e4m3 code of 2^x directly; both round P to e4m3, the default interpolates
+ * the exponential between powers of two first).  Slower; ignored elsewhere,
+ * where P always comes from v_exp_f32. */
+#define PCPA_FLAG_EXACT_EXP2 2u
 
 /* dtype codes. */
 #define PCPA_DTYPE_BF16 1

@@ -72,7 +72,9 @@ def _good_params(**kw):
         ({"pcp_size": 0}, -3),
         ({"num_q_heads": 7}, -3),
         ({"flags": 1}, 0),
-        ({"flags": 2}, -3),
+        ({"flags": 2}, 0),
+        ({"flags": 3}, 0),
+        ({"flags": 4}, -3),
         ({"q_dtype": 2}, -4),
         ({"kv_dtype": 9}, -4),
         ({"head_dim": 96}, -5),

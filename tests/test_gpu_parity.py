@@ -42,7 +42,7 @@ def _real_history(problem):
     return q, k, v
 
 
-def _run(problem, device, precision="auto"):
+def _run(problem, device, precision="auto", exp2="fast"):
     gpu = problem.to(device)
     kernel = make_history_attention_kernel(problem.config)
     out = kernel(
@@ -53,6 +53,7 @@ def _run(problem, device, precision="auto"):
         k_scale=problem.k_scale,
         v_scale=problem.v_scale,
         precision=precision,
+        exp2=exp2,
     )
     torch.cuda.synchronize()
     return out
@@ -208,3 +209,24 @@ def test_fp8_cache_both_mfma_precisions(precision, head_dim, cuda_device):
     q, k, v = _real_history(problem)
     _assert_close(out, orc.expected_stacked(q, k, v, orc.OracleShape.from_config(cfg)),
                   f"fp8 cache, {precision} MFMA, D={head_dim}")
+
+
+@pytest.mark.parametrize("exp2", ["fast", "exact"])
+@pytest.mark.parametrize("actual", [8192, 5000])
+def test_fp8_exp2_modes(exp2, actual, cuda_device):
+    """Both ways of forming the e4m3 probabilities (D=256 e4m3 path) against the
+    float64 oracle, aligned and with a partial last tile; the two results stay
+    close to each other as well."""
+    cfg = PCPAttentionConfig(
+        pcp_size=8, current_len=512, max_history_len=8192, actual_history_len=actual, block_size=256,
+        head_dim=256, backend="hip",
+    ).validate()
+    problem = build_paged_problem(cfg, seed=actual + 7, kv_scale="per_tensor")
+    out = _run(problem, cuda_device, precision="fp8", exp2=exp2).float().cpu().numpy()
+    q, k, v = _real_history(problem)
+    _assert_close(out, orc.expected_stacked(q, k, v, orc.OracleShape.from_config(cfg)),
+                  f"fp8 MFMA, exp2={exp2}, actual={actual}")
+    other = _run(problem, cuda_device, precision="fp8", exp2="exact" if exp2 == "fast" else "fast")
+    diff = np.abs(out - other.float().cpu().numpy())
+    print(f"fast vs exact exp2: max_abs={diff.max():.3e} mean_abs={diff.mean():.3e}", flush=True)
+    assert diff.max() <= MAX_ABS_TOL and diff.mean() <= MEAN_ABS_TOL
