@@ -7,10 +7,18 @@
 // online-softmax updates; here every query row walks the block table in
 // table order.
 //
+// Two kernels share the data layout and operand maps below:
+//   * history_fwd_kernel<D, STORE8, FP8>: 4 waves x 32 rows per workgroup,
+//     two workgroups per CU, double-buffered tiles; every head dim (64, 128,
+//     256) and precision (e4m3 or bf16 MFMAs).
+//   * ovl::history_fwd_overlap<256, FAST>: the e4m3-MFMA path at head_dim 256,
+//     8 waves x 32 rows, a two-stage in-wave pipeline with the two waves of a
+//     SIMD staggered by half a tile step (see its header).
+//
 // Work decomposition
 //   * A "row" is one (Q head, current token) pair.  Rows that share a KV head
-//     (GQA group) are independent and are tiled 128 to a workgroup:
-//     4 waves x 32 rows.  Grid = (ceil(rows_per_kv_head / 128), num_kv_heads).
+//     (GQA group) are independent and are tiled 32 to a wave; a workgroup's
+//     waves take consecutive row tiles of one KV head.
 //   * Keys are consumed in 64-key tiles staged through LDS (K tile and V tile,
 //     row-major [key][d], 16-byte chunks XOR-swizzled per key so that both the
 //     score-operand reads and the transposing V reads are bank-conflict free).
@@ -697,68 +705,18 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
 
 
 // ============================================================================
-// Software-pipelined FP8 kernel (head_dim 128 and 256): one wave per SIMD.
-//
-// gfx950 overlaps an MFMA with VALU work of the *same* wave almost
-// completely, but the MFMA of one wave with the VALU work of another wave on
-// the same SIMD only partly.  So each wave (32 query rows, the same work
-// split as history_fwd_kernel) runs its key tiles as a three-deep software
-// pipeline and interleaves, MFMA by MFMA, in iteration j:
-//
-//   X(j): S^T(j+2) = K(j+2) Q^T     with   softmax of tile j+1, first slices
-//   Y(j): O^T += V^T(j) P^T(j)      with   softmax of tile j+1, last slices
-//
-// and then rescales O^T if tile j+1 raised the running max (lazily, so
-// rarely).  Tiles before the first and after the last are "phantom" tiles
-// with no valid key: their scores are masked to -inf, their probabilities
-// are 0 and they leave the softmax state unchanged (the running max starts
-// at a finite floor), so one loop body serves the whole walk.  K and V tiles
-// live in separate four-stage LDS rings: tile t uses stage t % 4 of each.  At the top of iteration j the wave waits for K(j+2)
-// and V(j) (issued two iterations earlier), joins one barrier, and issues
-// K(j+4) and V(j+2) into stages that were last read two iterations ago.  The
-// loop is unrolled by four so that every LDS offset is an immediate.  V rows
-// past a partial tile's valid length are loaded from a zero chunk, so the
-// number of loads per tile (which the vmcnt waits count) never changes.
+// Helpers of the overlap kernel below.
 // ============================================================================
-namespace pipe {
+namespace ovl {
 
-constexpr int kThreads = 256;
-constexpr int kStages = 4;
 // Starting reference max: finite, so that a phantom tile (all scores -inf)
-// gives alpha = exp2(0) = 1 and probabilities exp2(-inf) = 0, and far below
-// any real score, so that the first real tile gives alpha = 0.
+// gives alpha = exp2(0) = 1 and probabilities of 0, and far below any real
+// score, so that the first real tile gives alpha = 0.
 constexpr float kMaxFloor = -1.0e30f;
 
 // A 16-byte chunk of zeros in global memory: the source of the V rows of a
 // partial tile that lie past its valid length.
 __device__ __attribute__((aligned(16))) uint8_t zero_chunk[16];
-
-template <int D>
-struct Shape {
-    static_assert(D == 128 || D == 256, "pipelined kernel covers head_dim 128 and 256");
-    static constexpr int ROW = D;            // e4m3 bytes of one key row (cache and LDS)
-    static constexpr int CHUNKS = D / 16;
-    static constexpr int TILE = kKeyTile * ROW;
-    static constexpr int RING = kStages * TILE;
-    static constexpr int QK = D / 64;         // k-steps of the score MFMA
-    static constexpr int NX = 2 * QK;         // score MFMAs per tile
-    static constexpr int DT = D / 32;         // PV MFMAs per tile
-    static constexpr int DPW = CHUNKS / 4;    // 1 KB DMA blocks per wave per K (or V) tile
-    static constexpr float RESCALE_LOG2 = 2.5f;
-    static constexpr int dma_key_delta(int i) { return ROW == 256 ? 16 * (i & 1) + 8 * (i >> 1) : 8 * i; }
-    // Softmax micro-slices [x_begin(i), x_begin(i+1)) run beside score MFMA
-    // i, and [y_begin(i), y_begin(i+1)) beside PV MFMA i (14 slices in all).
-    static constexpr int x_begin(int i) {
-        constexpr int b256[] = {0, 1, 2, 3, 5, 6, 7, 8, 9};
-        constexpr int b128[] = {0, 2, 4, 6, 7};
-        return D == 256 ? b256[i] : b128[i];
-    }
-    static constexpr int y_begin(int i) {
-        constexpr int b256[] = {9, 10, 11, 12, 13, 14, 14, 14, 14};
-        constexpr int b128[] = {7, 9, 11, 13, 14};
-        return D == 256 ? b256[i] : b128[i];
-    }
-};
 
 template <int I, int N, class F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -800,134 +758,11 @@ __device__ __forceinline__ void wait_vmem_le() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
-// Per-lane online-softmax state (log2 domain) plus the scratch of the
-// softmax in progress.
-struct SoftmaxRow {
-    float cscale;  // Q row scale * softmax_scale * k_scale * log2(e)
-    float m;       // reference max the probabilities are taken against
-    float l;       // this lane half's share of the running sum
-    float alpha;   // rescale factor of the last softmax (1: no change)
-    float mx, m_use, shift, psum;
-};
-
-// Micro-slice K of the online softmax of one score tile s (32 scores per
-// lane, masked keys already -inf).  0-3: running max over 8 scores each;
-// 4: new reference max (lags the tile max by at most RESCALE_LOG2, so the
-// probabilities stay below 2^(kPBiasLog2 + 2.5) = 362 < 448) and rescale
-// factor; 5-12: four probabilities each, packed into one e4m3 dword of P;
-// 13: running sum.
 // Empty asm statements pin a slice's results where the slice is written:
 // without them the compiler sinks the probabilities (used only in the next
 // iteration) below the PV MFMAs, and nothing overlaps.
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void pin(int& x) { asm volatile("" : "+v"(x)); }
-
-template <int D, int K>
-__device__ __forceinline__ void softmax_slice(const v16f (&s)[2], v8i& p, SoftmaxRow& sm) {
-    if constexpr (K < 4) {
-        constexpr int t = K >> 1, r = 8 * (K & 1);
-        float mx = max3(s[t][r], s[t][r + 1], s[t][r + 2]);
-        mx = max3(mx, s[t][r + 3], s[t][r + 4]);
-        mx = max3(mx, s[t][r + 5], s[t][r + 6]);
-        mx = K == 0 ? max3(mx, s[t][r + 7], s[t][r + 7]) : max3(mx, s[t][r + 7], sm.mx);
-        sm.mx = mx;
-        pin(sm.mx);
-    } else if constexpr (K == 4) {
-        const float mxs = halves_max(sm.mx) * sm.cscale;
-        sm.m_use = fmaxf(sm.m, mxs - Shape<D>::RESCALE_LOG2);
-        sm.alpha = __builtin_amdgcn_exp2f(sm.m - sm.m_use);
-        sm.shift = kPBiasLog2 - sm.m_use;
-        pin(sm.m_use);
-        pin(sm.alpha);
-        pin(sm.shift);
-    } else if constexpr (K < 13) {
-        constexpr int w = K - 5, t = w >> 2, r0 = 4 * (w & 3);
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[t][r0 + 0], sm.cscale, sm.shift));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(s[t][r0 + 1], sm.cscale, sm.shift));
-        const float p2 = __builtin_amdgcn_exp2f(fmaf(s[t][r0 + 2], sm.cscale, sm.shift));
-        const float p3 = __builtin_amdgcn_exp2f(fmaf(s[t][r0 + 3], sm.cscale, sm.shift));
-        const float part = (p0 + p1) + (p2 + p3);
-        sm.psum = w == 0 ? part : sm.psum + part;
-        // The first convert's untouched high half is overwritten by the
-        // second, so any register serves as its "old" operand.
-        const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(p0, p1, __float_as_int(p0), false);
-        int word = __builtin_amdgcn_cvt_pk_fp8_f32(p2, p3, pk, true);
-        pin(word);
-        pin(sm.psum);
-        p[w] = word;
-    } else {
-        sm.l = fmaf(sm.l, sm.alpha, sm.psum);
-        sm.m = sm.m_use;
-        pin(sm.l);
-        pin(sm.m);
-    }
-}
-
-template <int D, int LO, int HI>
-__device__ __forceinline__ void softmax_slices(const v16f (&s)[2], v8i& p, SoftmaxRow& sm) {
-    if constexpr (LO < HI) {
-        softmax_slice<D, LO>(s, p, sm);
-        softmax_slices<D, LO + 1, HI>(s, p, sm);
-    }
-}
-
-// Lane constants: LDS addresses of the score and PV A operands (stage 0,
-// chunk swizzle applied), and the lane's DMA chunk.
-template <int D>
-struct Lanes {
-    uint32_t k[Shape<D>::QK][2];  // score operand, k-step c, low/high 16 bytes (K ring)
-    uint32_t v[Shape<D>::DT];     // PV operand of d tile dt (V ring)
-    uint32_t dma_k[Shape<D>::DPW];  // byte offset of the lane's K chunk of DMA block i in a tile
-    uint32_t dma_v[Shape<D>::DPW];  // same for V (its own swizzle)
-    int dma_key;                    // key of the lane's chunk in DMA block 0
-};
-
-struct Cursors {
-    TileCursor c0, c1, c2, c3, c4;  // tiles j .. j+4 (e == num_entries: phantom)
-};
-
-// Issue the K tile of cursor c into K stage st.  Every lane loads one
-// 16-byte chunk per DMA block: tile base (uniform) + the lane's offset.
-// (The global and LDS pointers are formed in plain variables: address-space
-// casts of expressions that depend on S trip the host compilation pass.)
-template <class S>
-__device__ __forceinline__ void load_k_tile(const FwdArgs& a, const TileCursor& c, uint8_t* lds, int st,
-                                            int wave_off, const uint32_t (&off)[S::DPW]) {
-    const uint8_t* const tile = a.kv + c.k_off + (int64_t)c.base * S::ROW;
-    uint8_t* const dst = lds + st * S::TILE + wave_off;
-#pragma unroll
-    for (int i = 0; i < S::DPW; ++i) {
-        const uint8_t* const src = tile + off[i];
-        uint8_t* const d = dst + i * 4096;
-        __builtin_amdgcn_global_load_lds(src, PCPA_LDS(void, d), 16, 0, 0);
-    }
-}
-
-// Issue the V tile of cursor c into V stage st; rows past the valid length
-// come from zero_chunk (same number of loads either way).
-template <class S>
-__device__ __forceinline__ void load_v_tile(const FwdArgs& a, const TileCursor& c, uint8_t* lds, int st,
-                                            int wave_off, const uint32_t (&off)[S::DPW], int dma_key) {
-    const uint8_t* const tile = a.kv + c.k_off + (int64_t)c.base * S::ROW + (int64_t)a.num_kv_heads * a.head_stride;
-    uint8_t* const dst = lds + S::RING + st * S::TILE + wave_off;
-    if (c.n - c.base >= kKeyTile) {
-#pragma unroll
-        for (int i = 0; i < S::DPW; ++i) {
-            const uint8_t* const src = tile + off[i];
-            uint8_t* const d = dst + i * 4096;
-            __builtin_amdgcn_global_load_lds(src, PCPA_LDS(void, d), 16, 0, 0);
-        }
-    } else {
-        const uint8_t* const zero = zero_chunk;
-        const int lim = c.n - c.base - dma_key;  // the lane's chunk of block i is valid iff delta(i) < lim
-#pragma unroll
-        for (int i = 0; i < S::DPW; ++i) {
-            const uint8_t* const src = S::dma_key_delta(i) < lim ? tile + off[i] : zero;
-            uint8_t* const d = dst + i * 4096;
-            __builtin_amdgcn_global_load_lds(src, PCPA_LDS(void, d), 16, 0, 0);
-        }
-    }
-}
 
 // Scores of keys at or past `valid` become -inf.  Key of accumulator (t, r)
 // in lane half h: 32h + 16t + r (key_of_acc), compared as 16t + r against
@@ -941,290 +776,8 @@ __device__ __forceinline__ void mask_tail(v16f (&s)[2], int valid, int h) {
             if (16 * t + r >= lim) s[t][r] = -INFINITY;
 }
 
-// Iteration j of the pipeline, J4 = j mod 4; PV: j >= 0 (tile j is real).
-template <int D, int J4, bool PV>
-__device__ __forceinline__ void iteration(const FwdArgs& a, uint8_t* lds, int wave, int h, const Lanes<D>& L,
-                                          const v8i (&q)[Shape<D>::QK], v16f (&sbuf)[2][2], v8i (&pbuf)[2],
-                                          v16f (&o)[Shape<D>::DT], SoftmaxRow& sm, Cursors& cs, int head) {
-    using S = Shape<D>;
-    constexpr int KST = (J4 + 2) % kStages;  // K(j+2)
-    constexpr int VST = J4;                  // V(j)
-    constexpr int SN = J4 & 1;               // S(j+2), P(j) slots; S(j+1), P(j+1) are the others
-    v16f(&s_next)[2] = sbuf[SN];
-    v16f(&s_cur)[2] = sbuf[SN ^ 1];
-    v8i& p_cur = pbuf[SN];
-    v8i& p_next = pbuf[SN ^ 1];
+}  // namespace ovl
 
-    // ---- K(j+2) and V(j) have landed (for every wave) ----------------------
-    // Outstanding loads may be the ones issued one iteration ago: K(j+3) if
-    // tile j+3 exists, V(j+1) if tile j+1 exists.
-    {
-        const bool e1 = cs.c1.e < a.num_entries;
-        const bool e3 = cs.c3.e < a.num_entries;
-        if (e1 && e3)
-            wait_vmem_le<2 * S::DPW>();
-        else if (e1 || e3)
-            wait_vmem_le<S::DPW>();
-        else
-            wait_vmem_le<0>();
-    }
-    __builtin_amdgcn_s_barrier();
-    // The wave's LDS block offset is made opaque here so that the DMA
-    // destinations are recomputed with scalar adds each iteration rather than
-    // hoisted out of the loop and spilled.
-    int wave_off = wave * 1024;
-    asm volatile("" : "+s"(wave_off));
-    if (cs.c4.e < a.num_entries) load_k_tile<S>(a, cs.c4, lds, J4, wave_off, L.dma_k);
-    if (cs.c2.e < a.num_entries) load_v_tile<S>(a, cs.c2, lds, (J4 + 2) % kStages, wave_off, L.dma_v, L.dma_key);
-
-    {
-        const int valid1 = cs.c1.n - cs.c1.base;  // 0 for a phantom tile
-        if (valid1 < kKeyTile) mask_tail(s_cur, valid1, h);
-    }
-
-    // ---- X: S^T(j+2) with the first softmax slices of tile j+1 ------------
-    // Operand reads run two MFMAs ahead: before MFMA i the wave waits until
-    // only the reads of operand i+1 are outstanding (LDS returns in order;
-    // no scalar-memory load is in flight inside the phases).  The last X slot
-    // starts the first two V-operand reads of Y.
-    v2i xv[3][4];
-    auto issue_v = [&](auto dc) {
-        constexpr int dt = decltype(dc)::value;
-        constexpr int off = VST * S::TILE;
-        // keys 32g + 8s + m of the d tile live in LDS rows (8g + m) + {0, 32, 16, 48}[s]
-        xv[dt % 3][0] = ds_read_tr8_b64<off + 0 * S::ROW>(L.v[dt]);
-        xv[dt % 3][1] = ds_read_tr8_b64<off + 32 * S::ROW>(L.v[dt]);
-        xv[dt % 3][2] = ds_read_tr8_b64<off + 16 * S::ROW>(L.v[dt]);
-        xv[dt % 3][3] = ds_read_tr8_b64<off + 48 * S::ROW>(L.v[dt]);
-    };
-    {
-        v4i kr[3][2];
-        auto issue_k = [&](auto oc) {
-            constexpr int o = decltype(oc)::value, c = o >> 1, t = o & 1;
-            constexpr int off = KST * S::TILE + t * 16 * S::ROW;
-            kr[o % 3][0] = ds_read_b128<off>(L.k[c][0]);
-            kr[o % 3][1] = ds_read_b128<off>(L.k[c][1]);
-        };
-        // A phantom tile j+2 reads whatever its stage holds; the scores are
-        // masked before use.
-        issue_k(std::integral_constant<int, 0>{});
-        issue_k(std::integral_constant<int, 1>{});
-        static_for<0, S::NX>([&](auto oc) {
-            constexpr int o = decltype(oc)::value, c = o >> 1, t = o & 1;
-            if constexpr (o + 1 < S::NX) {
-                lds_wait<2>(kr[o % 3]);
-                if constexpr (o + 2 < S::NX) issue_k(std::integral_constant<int, o + 2>{});
-            } else {
-                lds_wait<0>(kr[o % 3]);
-                if constexpr (PV) {
-                    issue_v(std::integral_constant<int, 0>{});
-                    issue_v(std::integral_constant<int, 1>{});
-                }
-            }
-            const v4i lo = kr[o % 3][0], hi = kr[o % 3][1];
-            const v8i kop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            s_next[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kop, q[c], c == 0 ? v16f{} : s_next[t], 0,
-                                                                        0, 0, 0, 0, 0);
-            softmax_slices<D, S::x_begin(o), S::x_begin(o + 1)>(s_cur, p_next, sm);
-            __builtin_amdgcn_sched_barrier(0);
-        });
-    }
-
-    // ---- Y: O^T += V^T(j) P^T(j) with the last softmax slices of j+1 ------
-    static_for<0, S::DT>([&](auto dc) {
-        constexpr int dt = decltype(dc)::value;
-        if constexpr (PV) {
-            if constexpr (dt + 1 < S::DT) {
-                lds_wait<4>(xv[dt % 3]);
-                if constexpr (dt + 2 < S::DT) issue_v(std::integral_constant<int, dt + 2>{});
-            } else {
-                lds_wait<0>(xv[dt % 3]);
-            }
-            const v2i(&x)[4] = xv[dt % 3];
-            const v8i vop = {x[0][0], x[0][1], x[1][0], x[1][1], x[2][0], x[2][1], x[3][0], x[3][1]};
-            o[dt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vop, p_cur, o[dt], 0, 0, 0, 0, 0, 0);
-        }
-        softmax_slices<D, S::y_begin(dt), S::y_begin(dt + 1)>(s_cur, p_next, sm);
-        __builtin_amdgcn_sched_barrier(0);
-    });
-
-    // ---- O^T to tile j+1's reference max ----------------------------------
-    if (__builtin_amdgcn_ballot_w64(sm.alpha < 1.f) != 0) {
-#pragma unroll
-        for (int dt = 0; dt < S::DT; ++dt) o[dt] *= sm.alpha;
-    }
-
-    cs.c0 = cs.c1;
-    cs.c1 = cs.c2;
-    cs.c2 = cs.c3;
-    cs.c3 = cs.c4;
-    if (cs.c4.e < a.num_entries) cs.c4 = next_tile(a, head, cs.c4);
-}
-
-template <int D>
-__global__ void __launch_bounds__(kThreads, 1) history_fwd_pipelined(FwdArgs a) {
-    using S = Shape<D>;
-    constexpr int QK = S::QK, DT = S::DT, ROW = S::ROW, CHUNKS = S::CHUNKS;
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * S::RING];
-
-    // ---- XCD-aware work mapping (as history_fwd_kernel) ---------------------
-    const int items = a.row_tiles * a.num_kv_heads;
-    const int per_xcd = (items + 7) / 8;
-    const int item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-    if (item >= items) return;
-    const int head = item / a.row_tiles;
-    const int row_tile = item - head * a.row_tiles;
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int j = lane & 31;
-    const int h = lane >> 5;
-    const int grp = lane >> 4;
-    const int gl = lane & 15;
-
-    // ---- this lane's query row and its e4m3 Q^T operand ---------------------
-    const int row = row_tile * kRowsPerGroup + wave * kRowsPerWave + j;
-    const bool row_ok = row < a.rows_per_head;
-    const int rowc = row_ok ? row : a.rows_per_head - 1;
-    const int rank = rowc / a.group_rows;
-    const int rem = rowc - rank * a.group_rows;
-    const int head_in_group = rem / a.local_q;
-    const int tok = rem - head_in_group * a.local_q;
-    const int64_t row_off =
-        ((int64_t)(rank * a.num_q_heads + head * a.group + head_in_group) * a.local_q + tok) * D * 2;
-    const uint8_t* const qrow = a.q + row_off;
-
-    v8i q[QK];
-    SoftmaxRow sm;
-    {
-        // lane (j, h) holds d = 64c + 32h + [0, 32) of its row, as e4m3.
-        float amax = 0.f;
-#pragma unroll
-        for (int c = 0; c < QK; ++c)
-#pragma unroll
-            for (int part = 0; part < 4; ++part) {
-                const v4i raw = *(const v4i*)(qrow + (64 * c + 32 * h) * 2 + 16 * part);
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    const uint32_t u = (uint32_t)raw[w];
-                    amax = fmaxf(amax, fabsf(bf16_bits_to_f32(u & 0xffffu)));
-                    amax = fmaxf(amax, fabsf(bf16_bits_to_f32(u >> 16)));
-                }
-            }
-        amax = halves_max(amax);
-        const float inv = amax > 0.f ? kFp8Max / amax : 1.f;
-        const float sigma = amax > 0.f ? amax / kFp8Max : 1.f;
-#pragma unroll
-        for (int c = 0; c < QK; ++c)
-#pragma unroll
-            for (int part = 0; part < 4; ++part) {
-                const v4i raw = *(const v4i*)(qrow + (64 * c + 32 * h) * 2 + 16 * part);
-#pragma unroll
-                for (int w = 0; w < 2; ++w) {
-                    const uint32_t u0 = (uint32_t)raw[2 * w], u1 = (uint32_t)raw[2 * w + 1];
-                    int pk = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_bits_to_f32(u0 & 0xffffu) * inv,
-                                                             bf16_bits_to_f32(u0 >> 16) * inv, 0, false);
-                    pk = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_bits_to_f32(u1 & 0xffffu) * inv,
-                                                         bf16_bits_to_f32(u1 >> 16) * inv, pk, true);
-                    q[c][2 * part + w] = pk;
-                }
-            }
-        sm.cscale = sigma * a.score_scale;
-        sm.m = kMaxFloor;
-        sm.l = 0.f;
-        sm.alpha = 1.f;
-    }
-
-    // ---- lane constants ------------------------------------------------------
-    Lanes<D> L;
-    {
-        const uint32_t base = lds_address(lds);
-        const int krow = lds_row<true>(key_of_row<true>(0, j));
-        const uint32_t k_addr = krow * ROW + (((2 * h) ^ chunk_swizzle<true, CHUNKS>(krow)) << 4);
-#pragma unroll
-        for (int c = 0; c < QK; ++c)
-#pragma unroll
-            for (int hl = 0; hl < 2; ++hl) L.k[c][hl] = base + (k_addr ^ ((4 * c + hl) << 4));
-        // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1): key 32*(grp>>1) + (gl>>1)
-        const int vrow = lds_row<true>(32 * (grp >> 1) + (gl >> 1));
-        const uint32_t v_addr = vrow * ROW + (((grp & 1) ^ chunk_swizzle_v<true, CHUNKS>(vrow)) << 4) + 8 * (gl & 1);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) L.v[dt] = base + S::RING + (v_addr ^ ((2 * dt) << 4));
-        // DMA block 4i + wave lands at LDS row R0 + (4i * 1024 / ROW); its key is
-        // the lane's block-0 key plus dma_key_delta(i), with the same swizzle.
-        const int byte = wave * 1024 + lane * 16;
-        const int drow = byte / ROW;
-        const int pos = (byte % ROW) / 16;
-        L.dma_key = lds_row<true>(drow);
-        const uint32_t k0 = L.dma_key * ROW + (pos ^ chunk_swizzle<true, CHUNKS>(drow)) * 16;
-        const uint32_t v0 = L.dma_key * ROW + (pos ^ chunk_swizzle_v<true, CHUNKS>(drow)) * 16;
-#pragma unroll
-        for (int i = 0; i < S::DPW; ++i) {
-            L.dma_k[i] = k0 + S::dma_key_delta(i) * ROW;
-            L.dma_v[i] = v0 + S::dma_key_delta(i) * ROW;
-        }
-    }
-
-    v16f o[DT];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] = v16f{};
-    v16f sbuf[2][2];
-    v8i pbuf[2];
-
-    // ---- pipeline --------------------------------------------------------------
-    const TileCursor none{a.num_entries, 0, 0, 0};
-    Cursors cs;
-    cs.c0 = none;  // tile -2
-    cs.c1 = none;  // tile -1
-    cs.c2 = next_tile(a, head, TileCursor{-1, 0, 0, 0});
-    if (cs.c2.e < a.num_entries) {
-        cs.c3 = next_tile(a, head, cs.c2);
-        cs.c4 = cs.c3.e < a.num_entries ? next_tile(a, head, cs.c3) : none;
-        // K(0) and K(1), as if issued at the top of iterations -4 and -3.
-        load_k_tile<S>(a, cs.c2, lds, 0, wave * 1024, L.dma_k);
-        if (cs.c3.e < a.num_entries) load_k_tile<S>(a, cs.c3, lds, 1, wave * 1024, L.dma_k);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) pbuf[i] = v8i{};
-
-        iteration<D, 2, false>(a, lds, wave, h, L, q, sbuf, pbuf, o, sm, cs, head);  // j = -2: S(0)
-        iteration<D, 3, false>(a, lds, wave, h, L, q, sbuf, pbuf, o, sm, cs, head);  // j = -1: S(1), P(0)
-        for (;;) {  // j = 0, 1, ...: runs while tile j exists
-            iteration<D, 0, true>(a, lds, wave, h, L, q, sbuf, pbuf, o, sm, cs, head);
-            if (cs.c0.e >= a.num_entries) break;
-            iteration<D, 1, true>(a, lds, wave, h, L, q, sbuf, pbuf, o, sm, cs, head);
-            if (cs.c0.e >= a.num_entries) break;
-            iteration<D, 2, true>(a, lds, wave, h, L, q, sbuf, pbuf, o, sm, cs, head);
-            if (cs.c0.e >= a.num_entries) break;
-            iteration<D, 3, true>(a, lds, wave, h, L, q, sbuf, pbuf, o, sm, cs, head);
-            if (cs.c0.e >= a.num_entries) break;
-        }
-    }
-
-    // ---- epilogue: O = O^T / l, bf16 -----------------------------------------
-    const float l_tot = halves_sum(sm.l);
-    const float scale = l_tot > 0.f ? a.v_scale / l_tot : 0.f;
-    if (row_ok) {
-        uint8_t* const orow = a.out + row_off;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const int d = 32 * dt + 8 * r4 + 4 * h;
-                const __bf16 v0 = (__bf16)(o[dt][4 * r4 + 0] * scale);
-                const __bf16 v1 = (__bf16)(o[dt][4 * r4 + 1] * scale);
-                const __bf16 v2 = (__bf16)(o[dt][4 * r4 + 2] * scale);
-                const __bf16 v3 = (__bf16)(o[dt][4 * r4 + 3] * scale);
-                const uint32_t w0 = (uint32_t)__builtin_bit_cast(uint16_t, v0) |
-                                    ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16);
-                const uint32_t w1 = (uint32_t)__builtin_bit_cast(uint16_t, v2) |
-                                    ((uint32_t)__builtin_bit_cast(uint16_t, v3) << 16);
-                *(v2i*)(orow + 2 * d) = v2i{(int)w0, (int)w1};
-            }
-    }
-}
-
-}  // namespace pipe
 
 // ============================================================================
 // FP8 kernel with an in-wave MFMA/softmax overlap (head_dim 128 and 256).
@@ -1331,21 +884,21 @@ template <int K, bool FAST>
 __device__ __forceinline__ void softmax_slice(const v16f (&s)[2], v8i& p, SoftmaxRow& sm) {
     if constexpr (K < 4) {
         constexpr int t = K >> 1, r = 8 * (K & 1);
-        float mx = pipe::max3(s[t][r], s[t][r + 1], s[t][r + 2]);
-        mx = pipe::max3(mx, s[t][r + 3], s[t][r + 4]);
-        mx = pipe::max3(mx, s[t][r + 5], s[t][r + 6]);
-        mx = K == 0 ? pipe::max3(mx, s[t][r + 7], s[t][r + 7]) : pipe::max3(mx, s[t][r + 7], sm.mx);
+        float mx = max3(s[t][r], s[t][r + 1], s[t][r + 2]);
+        mx = max3(mx, s[t][r + 3], s[t][r + 4]);
+        mx = max3(mx, s[t][r + 5], s[t][r + 6]);
+        mx = K == 0 ? max3(mx, s[t][r + 7], s[t][r + 7]) : max3(mx, s[t][r + 7], sm.mx);
         sm.mx = mx;
-        pipe::pin(sm.mx);
+        pin(sm.mx);
     } else if constexpr (K == 4) {
         const float mxs = halves_max(sm.mx) * sm.cscale;
         sm.m_use = fmaxf(sm.m, mxs - 2.5f);
         sm.alpha = __builtin_amdgcn_exp2f(sm.m - sm.m_use);
         // FAST: 8x + 56 = s * 8 cscale + (8 (6 - m_use) + 56)
         sm.shift = FAST ? fmaf(-8.f, sm.m_use, 8.f * kPBiasLog2 + 56.f) : kPBiasLog2 - sm.m_use;
-        pipe::pin(sm.m_use);
-        pipe::pin(sm.alpha);
-        pipe::pin(sm.shift);
+        pin(sm.m_use);
+        pin(sm.alpha);
+        pin(sm.shift);
     } else if constexpr (K < 13) {
         constexpr int w = K - 5, t = w >> 2, r0 = 4 * (w & 3);
         int word;
@@ -1364,11 +917,11 @@ __device__ __forceinline__ void softmax_slice(const v16f (&s)[2], v8i& p, Softma
             const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(p0, p1, __float_as_int(p0), false);
             word = __builtin_amdgcn_cvt_pk_fp8_f32(p2, p3, pk, true);
         }
-        pipe::pin(word);
+        pin(word);
         p[w] = word;
     } else {
         sm.m = sm.m_use;
-        pipe::pin(sm.m);
+        pin(sm.m);
     }
 }
 
@@ -1421,7 +974,7 @@ __device__ __forceinline__ void load_v(const FwdArgs& a, const TileCursor& c, ui
             __builtin_amdgcn_global_load_lds(src, PCPA_LDS(void, d), 16, 0, 0);
         }
     } else {
-        const uint8_t* const zero = pipe::zero_chunk;
+        const uint8_t* const zero = zero_chunk;
 #pragma unroll
         for (int i = 0; i < S::DPW; ++i) {
             const uint8_t* const src =
@@ -1452,13 +1005,13 @@ __device__ __forceinline__ void s_half(uint32_t k_addr, uint32_t v_addr, const v
     auto issue_k = [&](auto oc) {
         constexpr int op = decltype(oc)::value, c = op >> 1, t = op & 1;
         constexpr int off = KST * S::TILE + t * 16 * S::ROW;
-        kr[op & 1][0] = pipe::ds_read_b128<off>(k_addr ^ ((4 * c) << 4));
-        kr[op & 1][1] = pipe::ds_read_b128<off>(k_addr ^ ((4 * c + 1) << 4));
+        kr[op & 1][0] = ds_read_b128<off>(k_addr ^ ((4 * c) << 4));
+        kr[op & 1][1] = ds_read_b128<off>(k_addr ^ ((4 * c + 1) << 4));
     };
     issue_k(std::integral_constant<int, 0>{});
-    pipe::static_for<0, S::NX>([&](auto oc) {
+    static_for<0, S::NX>([&](auto oc) {
         constexpr int op = decltype(oc)::value, c = op >> 1, t = op & 1;
-        pipe::lds_wait<0>(kr[op & 1]);
+        lds_wait<0>(kr[op & 1]);
         if constexpr (op + 1 < S::NX) {
             issue_k(std::integral_constant<int, op + 1>{});
         } else if constexpr (PREFETCH_V) {
@@ -1487,7 +1040,7 @@ template <int D, int VST, bool PREFETCHED, bool FAST>
 __device__ __forceinline__ void pv_half(uint32_t v_addr, v2i (&xv0)[4], v16f (&o)[Shape<D>::DT], const v8i& p_old,
                                         v16f (&s)[2], v8i& p_new, SoftmaxRow& sm, int valid, int h) {
     using S = Shape<D>;
-    if (valid < kKeyTile) pipe::mask_tail(s, valid, h);
+    if (valid < kKeyTile) mask_tail(s, valid, h);
     v2i xv1[4];
     auto buf = [&](auto dc) -> v2i(&)[4] {
         if constexpr ((decltype(dc)::value & 1) == 0)
@@ -1506,10 +1059,10 @@ __device__ __forceinline__ void pv_half(uint32_t v_addr, v2i (&xv0)[4], v16f (&o
         x[3] = ds_read_tr8_b64<off + 48 * S::ROW>(addr);
     };
     if constexpr (!PREFETCHED) issue_v(std::integral_constant<int, 0>{});
-    pipe::static_for<0, S::DT>([&](auto dc) {
+    static_for<0, S::DT>([&](auto dc) {
         constexpr int dt = decltype(dc)::value;
         v2i(&x)[4] = buf(dc);
-        pipe::lds_wait<0>(x);
+        lds_wait<0>(x);
         if constexpr (dt + 1 < S::DT) issue_v(std::integral_constant<int, dt + 1>{});
         const v8i vop = {x[0][0], x[0][1], x[1][0], x[1][1], x[2][0], x[2][1], x[3][0], x[3][1]};
         o[dt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vop, p_old, o[dt], 0, 0, 0, 0, 0, 0);
@@ -1537,9 +1090,9 @@ __device__ __forceinline__ void iteration(const FwdArgs& a, uint8_t* lds, int wa
     // Loads issued one iteration ago may be pending: V(j), and K(j+1) if tile
     // j+1 is real.
     if (is_real(a, cs.c1))
-        pipe::wait_vmem_le<2 * S::DPW>();
+        wait_vmem_le<2 * S::DPW>();
     else
-        pipe::wait_vmem_le<S::DPW>();
+        wait_vmem_le<S::DPW>();
     __builtin_amdgcn_s_barrier();
     // K stage (j+2) % 4 held K(j-2) and V stage (j+1) % 4 held V(j-3); both
     // were last read in iteration j-1.  The wave offset and operand bases
@@ -1665,7 +1218,7 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
             }
         sm.cscale = sigma * a.score_scale;
         sm.cscale8 = 8.f * sm.cscale;
-        sm.m = pipe::kMaxFloor;
+        sm.m = kMaxFloor;
         sm.l = 0.f;
         sm.alpha = 1.f;
     }

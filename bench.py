@@ -31,6 +31,9 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 METRIC = "ms + TFLOP/s (% FP8 MFMA peak), Q=4K x 128K paged FP8 KV history, 1 GPU"
+# HBM bytes per launch measured with rocprofv3 PMC counters (FETCH_SIZE and
+# WRITE_SIZE, each calibrated on a copy kernel of known size).
+TRAFFIC_FILE = ROOT / "profiles" / "pmc_traffic.txt"
 # MI355X published dense MFMA peaks, TFLOP/s.
 PEAK_TFLOPS = {"fp8_e4m3fn": 5000.0, "bfloat16": 2500.0}
 HBM_PEAK_GBS = 8000.0
@@ -65,6 +68,19 @@ def copy_probe(mib: int, steps: int) -> int:
     torch.cuda.synchronize()
     print(json.dumps({"copy_probe_bytes": src.numel(), "steps": steps}), flush=True)
     return 0
+
+
+def measured_traffic(workload: str):
+    """(bytes, source) for ``workload`` from TRAFFIC_FILE, or (None, None)."""
+    if not TRAFFIC_FILE.exists():
+        return None, None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        fields = line.split()
+        if len(fields) == 6 and not line.startswith("#") and fields[0] == workload:
+            fetch = float(fields[2]) * 1024 * float(fields[3])
+            write = float(fields[4]) * 1024 * float(fields[5])
+            return fetch + write, f"{TRAFFIC_FILE.relative_to(ROOT)} ({fields[1]})"
+    return None, None
 
 
 def model_flops(cfg) -> float:
@@ -173,6 +189,8 @@ def main(argv=None) -> int:
     peak = PEAK_TFLOPS[cfg.kv_dtype]
     achieved = flops / (kernel_ms * 1e-3) / 1e12
     p90 = launch_ms[max(0, (9 * len(launch_ms) + 9) // 10 - 1)]
+    traffic, traffic_source = (args.traffic_bytes, "--traffic-bytes") if args.traffic_bytes else \
+        measured_traffic(workload.name)
 
     result = {
         "metric": METRIC,
@@ -212,7 +230,8 @@ def main(argv=None) -> int:
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4),
-            "traffic": args.traffic_bytes,
+            "traffic": traffic,
+            "traffic_source": traffic_source,
             "algorithmic_bytes": algorithmic_bytes(cfg),
             "algorithmic_hbm_gbs": round(algorithmic_bytes(cfg) / (kernel_ms * 1e-3) / 1e9, 1),
         },
