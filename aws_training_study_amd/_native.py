@@ -43,6 +43,8 @@ EXPORTED_SYMBOLS = (
     "pcpa_status_string",
     "pcpa_check_params",
     "pcpa_history_attention",
+    "pcpa_kv_cache_write",
+    "pcpa_absmax_bf16",
 )
 
 
@@ -113,6 +115,21 @@ def load_library() -> ctypes.CDLL:
         ctypes.c_void_p,
         ctypes.c_void_p,
     ]
+    lib.pcpa_kv_cache_write.restype = ctypes.c_int32
+    lib.pcpa_kv_cache_write.argtypes = [
+        ctypes.POINTER(PcpaParams),
+        ctypes.c_int32,
+        ctypes.c_int64,
+        ctypes.c_int32,
+        ctypes.c_void_p,
+        ctypes.c_void_p,
+        ctypes.c_void_p,
+        ctypes.c_void_p,
+        ctypes.c_void_p,
+        ctypes.c_void_p,
+    ]
+    lib.pcpa_absmax_bf16.restype = ctypes.c_int32
+    lib.pcpa_absmax_bf16.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
     version = lib.pcpa_abi_version()
     if version != ABI_VERSION:
         raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}; rebuild it")

@@ -1300,6 +1300,169 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
 // ============================================================================
 // C ABI
 // ============================================================================
+
+// ============================================================================
+// KV-cache producer: per-tensor e4m3 quantisation of K/V and the page write
+// in pack_local_kv's format (kernel.py:17-29), i.e. what the reference does
+// on the host with shard_history (layout.py:54-98), the float8 cast
+// (run_poc.py:96-103) and pack_local_kv, done on the GPU for a range of
+// global history positions (a whole history, or tokens appended to it).
+// Both kernels are HBM bound: 2 bytes read and 1 (e4m3) or 2 (bf16) bytes
+// written per element.
+// ============================================================================
+namespace pcpa {
+namespace cache {
+
+constexpr int kThreads = 256;
+
+// floor(n / d) for 0 <= n < 2^31 by one 64-bit multiply: M = ceil(2^(32+s)/d)
+// with 2^s >= d gives the exact quotient for every n < 2^32.
+struct FastDiv {
+    uint64_t m;
+    uint32_t shift;
+    uint32_t d;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t s = 0;
+    while ((1ull << s) < d) ++s;
+    const unsigned __int128 num = (unsigned __int128)1 << (32 + s);
+    return FastDiv{(uint64_t)((num + d - 1) / d), 32 + s, d};
+}
+__device__ __forceinline__ uint32_t div(uint32_t n, const FastDiv& f) {
+    return (uint32_t)(((unsigned __int128)n * f.m) >> f.shift);
+}
+
+struct WriteArgs {
+    const uint8_t* k;   // [Hkv, n, D] bf16
+    const uint8_t* v;
+    const int32_t* block_table;
+    int32_t* page_valid_len;  // optional
+    uint8_t* pages;
+    int64_t page_stride;      // bytes of one page
+    int64_t head_stride;      // bytes of one head's K (or V) block in a page
+    int64_t v_offset;         // bytes from a page's K to its V
+    FastDiv chunks_per_row;   // D / 8
+    FastDiv interleave;
+    FastDiv pcp;
+    FastDiv block;            // block_size
+    uint32_t log2_cpr, log2_il, log2_pcp, log2_block;  // when POW2
+    uint32_t num_tokens;
+    uint32_t first_pos;
+    int32_t max_local_blocks;
+    int32_t num_pages;
+    int32_t head_dim;
+    float k_scale, v_scale;
+};
+
+// e4m3 code of x (round to nearest even; magnitudes above 464 and infinities
+// become the NaN code 0x7f with x's sign, like torch's float8_e4m3fn cast;
+// v_cvt_pk_fp8_f32 agrees except that it writes 0xff for every NaN input).
+__device__ __forceinline__ uint32_t e4m3_codes4(float a, float b, float c, float d) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    uint32_t u = (uint32_t)w;
+    const float x[4] = {a, b, c, d};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (__builtin_isnan(x[i])) {
+            const uint32_t code = (__float_as_uint(x[i]) >> 31) ? 0xffu : 0x7fu;
+            u = (u & ~(0xffu << (8 * i))) | (code << (8 * i));
+        }
+    return u;
+}
+
+// One thread per (token, 8-element chunk) of head blockIdx.y: the token's
+// page row comes from the striped layout (owner rank, local position) and
+// the block table.  POW2: pcp, interleave, block size and D / 8 are powers
+// of two (every configuration in use), so the maps are shifts and masks.
+// Tokens whose table entry is outside [0, num_pages) are skipped, as the
+// attention kernel skips such pages.
+template <bool FP8, bool POW2>
+__global__ void __launch_bounds__(kThreads) kv_write_kernel(WriteArgs a, uint32_t row_chunks) {
+    const uint32_t gid = blockIdx.x * kThreads + threadIdx.x;
+    if (gid >= row_chunks) return;
+    const uint32_t head = blockIdx.y;
+    uint32_t token, chunk, owner, local, blk, slot;
+    const uint32_t p0 = a.first_pos;
+    if constexpr (POW2) {
+        token = gid >> a.log2_cpr;
+        chunk = gid & ((1u << a.log2_cpr) - 1);
+        const uint32_t p = p0 + token;
+        const uint32_t c = p >> a.log2_il;
+        owner = c & ((1u << a.log2_pcp) - 1);
+        local = ((c >> a.log2_pcp) << a.log2_il) | (p & ((1u << a.log2_il) - 1));
+        blk = local >> a.log2_block;
+        slot = local & ((1u << a.log2_block) - 1);
+    } else {
+        token = div(gid, a.chunks_per_row);
+        chunk = gid - token * a.chunks_per_row.d;
+        const uint32_t p = p0 + token;
+        const uint32_t c = div(p, a.interleave);
+        const uint32_t rounds = div(c, a.pcp);
+        owner = c - rounds * a.pcp.d;
+        local = rounds * a.interleave.d + (p - c * a.interleave.d);
+        blk = div(local, a.block);
+        slot = local - blk * a.block.d;
+    }
+    const uint32_t row = head * a.num_tokens + token;
+    if (blk >= (uint32_t)a.max_local_blocks) return;  // excluded by the host's capacity check
+    const int32_t entry = (int32_t)(owner * a.max_local_blocks + blk);
+    const int32_t page = a.block_table[entry];
+    if ((uint32_t)page >= (uint32_t)a.num_pages) return;
+    if (a.page_valid_len && head == 0 && chunk == 0) atomicMax(a.page_valid_len + entry, (int32_t)slot + 1);
+
+    const int64_t src = ((int64_t)row * a.head_dim + chunk * 8) * 2;  // [Hkv, n, D] bf16
+    const v4i kin = *(const v4i*)(a.k + src);
+    const v4i vin = *(const v4i*)(a.v + src);
+    const int64_t es = FP8 ? 1 : 2;
+    uint8_t* const dst = a.pages + (int64_t)page * a.page_stride + head * a.head_stride +
+                         ((int64_t)slot * a.head_dim + chunk * 8) * es;
+    if constexpr (FP8) {
+        float kf[8], vf[8];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            // x / scale with IEEE division, as torch computes (x / scale).to(float8)
+            kf[2 * w] = bf16_bits_to_f32((uint32_t)kin[w] & 0xffffu) / a.k_scale;
+            kf[2 * w + 1] = bf16_bits_to_f32((uint32_t)kin[w] >> 16) / a.k_scale;
+            vf[2 * w] = bf16_bits_to_f32((uint32_t)vin[w] & 0xffffu) / a.v_scale;
+            vf[2 * w + 1] = bf16_bits_to_f32((uint32_t)vin[w] >> 16) / a.v_scale;
+        }
+        *(v2i*)dst = v2i{(int)e4m3_codes4(kf[0], kf[1], kf[2], kf[3]), (int)e4m3_codes4(kf[4], kf[5], kf[6], kf[7])};
+        *(v2i*)(dst + a.v_offset) =
+            v2i{(int)e4m3_codes4(vf[0], vf[1], vf[2], vf[3]), (int)e4m3_codes4(vf[4], vf[5], vf[6], vf[7])};
+    } else {
+        *(v4i*)dst = kin;
+        *(v4i*)(dst + a.v_offset) = vin;
+    }
+}
+
+// max |x| over n bf16 values into *out (as the bits of a non-negative float,
+// ordered like unsigned integers); *out is cleared first by init_kernel.
+__global__ void absmax_init_kernel(uint32_t* out) { *out = 0u; }
+
+__global__ void __launch_bounds__(kThreads) absmax_kernel(const uint16_t* x, int64_t n, uint32_t* out) {
+    float m = 0.f;
+    const int64_t stride = (int64_t)gridDim.x * kThreads * 8;
+    for (int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 8; i < n; i += stride) {
+        if (i + 8 <= n) {
+            const v4i raw = *(const v4i*)(x + i);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                m = fmaxf(m, fabsf(bf16_bits_to_f32((uint32_t)raw[w] & 0xffffu)));
+                m = fmaxf(m, fabsf(bf16_bits_to_f32((uint32_t)raw[w] >> 16)));
+            }
+        } else {
+            for (int64_t e = i; e < n; ++e) m = fmaxf(m, fabsf(bf16_bits_to_f32(x[e])));
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((threadIdx.x & 63) == 0) atomicMax(out, __float_as_uint(m));
+}
+
+}  // namespace cache
+}  // namespace pcpa
+
 extern "C" {
 
 int32_t pcpa_abi_version(void) { return PCPA_ABI_VERSION; }
@@ -1406,6 +1569,92 @@ int32_t pcpa_history_attention(const pcpa_params* p, const void* q, const void* 
     }
     const hipError_t err = hipLaunchKernel(fn, grid, block, args, 0, (hipStream_t)stream);
     return err == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
+}
+
+
+int32_t pcpa_absmax_bf16(const void* x, int64_t n, float* amax, void* stream) {
+    if (!x || !amax) return PCPA_ERR_NULL_POINTER;
+    if (n < 0) return PCPA_ERR_BAD_SHAPE;
+    if (((uintptr_t)x & 15u) || ((uintptr_t)amax & 3u)) return PCPA_ERR_MISALIGNED;
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(pcpa::cache::absmax_init_kernel, dim3(1), dim3(1), 0, st, (uint32_t*)amax);
+    if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
+    if (n == 0) return PCPA_OK;
+    const int64_t groups = (n + 8 * pcpa::cache::kThreads - 1) / (8 * pcpa::cache::kThreads);
+    const unsigned blocks = (unsigned)(groups < 2048 ? groups : 2048);
+    hipLaunchKernelGGL(pcpa::cache::absmax_kernel, dim3(blocks), dim3(pcpa::cache::kThreads), 0, st,
+                       (const uint16_t*)x, n, (uint32_t*)amax);
+    return hipGetLastError() == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
+}
+
+int32_t pcpa_kv_cache_write(const pcpa_params* p, int32_t interleave, int64_t first_pos, int32_t num_tokens,
+                            const void* k, const void* v, const int32_t* block_table, void* kv_pages,
+                            int32_t* page_valid_len, void* stream) {
+    const int32_t st = pcpa_check_params(p);
+    if (st != PCPA_OK) return st;
+    if (!k || !v || !block_table || !kv_pages) return PCPA_ERR_NULL_POINTER;
+    if (interleave <= 0 || first_pos < 0 || num_tokens < 0) return PCPA_ERR_BAD_SHAPE;
+    if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)kv_pages) & 15u) return PCPA_ERR_MISALIGNED;
+    if (((uintptr_t)block_table | (uintptr_t)page_valid_len) & 3u) return PCPA_ERR_MISALIGNED;
+    if (num_tokens == 0) return PCPA_OK;
+    // Every position must have a cache block: local index < max_local_blocks *
+    // block_size.  The local index grows with the position for each owner
+    // rank, so the largest one is among the last pcp_size * interleave
+    // positions of the range.
+    const int64_t capacity = (int64_t)p->max_local_blocks * p->block_size;  // per rank
+    const int64_t last = first_pos + num_tokens - 1;
+    const int64_t round_len = (int64_t)p->pcp_size * interleave;
+    for (int64_t pos = last; pos >= first_pos && pos > last - round_len; --pos) {
+        const int64_t chunk = pos / interleave;
+        if ((chunk / p->pcp_size) * interleave + pos % interleave >= capacity) return PCPA_ERR_BAD_SHAPE;
+    }
+    const int64_t chunks = (int64_t)p->num_kv_heads * num_tokens * (p->head_dim / 8);
+    if (last >= INT32_MAX || chunks > INT32_MAX || (int64_t)p->pcp_size * capacity > INT32_MAX)
+        return PCPA_ERR_TOO_LARGE;
+
+    const bool fp8 = p->kv_dtype == PCPA_DTYPE_FP8_E4M3FN;
+    const int64_t es = fp8 ? 1 : 2;
+    pcpa::cache::WriteArgs a;
+    a.k = (const uint8_t*)k;
+    a.v = (const uint8_t*)v;
+    a.block_table = block_table;
+    a.page_valid_len = page_valid_len;
+    a.pages = (uint8_t*)kv_pages;
+    a.head_stride = (int64_t)p->block_size * p->head_dim * es;
+    a.v_offset = (int64_t)p->num_kv_heads * a.head_stride;
+    a.page_stride = 2 * a.v_offset;
+    a.chunks_per_row = pcpa::cache::make_fastdiv((uint32_t)(p->head_dim / 8));
+    a.interleave = pcpa::cache::make_fastdiv((uint32_t)interleave);
+    a.pcp = pcpa::cache::make_fastdiv((uint32_t)p->pcp_size);
+    a.block = pcpa::cache::make_fastdiv((uint32_t)p->block_size);
+    auto log2_of = [](uint32_t x) -> int { return (x & (x - 1)) ? -1 : __builtin_ctz(x); };
+    const int l_cpr = log2_of((uint32_t)(p->head_dim / 8)), l_il = log2_of((uint32_t)interleave);
+    const int l_pcp = log2_of((uint32_t)p->pcp_size), l_blk = log2_of((uint32_t)p->block_size);
+    const bool pow2 = l_cpr >= 0 && l_il >= 0 && l_pcp >= 0 && l_blk >= 0;
+    a.log2_cpr = pow2 ? l_cpr : 0;
+    a.log2_il = pow2 ? l_il : 0;
+    a.log2_pcp = pow2 ? l_pcp : 0;
+    a.log2_block = pow2 ? l_blk : 0;
+    a.num_tokens = (uint32_t)num_tokens;
+    a.first_pos = (uint32_t)first_pos;
+    a.max_local_blocks = p->max_local_blocks;
+    a.num_pages = p->num_pages;
+    a.head_dim = p->head_dim;
+    a.k_scale = p->k_scale;
+    a.v_scale = p->v_scale;
+    const uint32_t row_chunks = (uint32_t)num_tokens * (uint32_t)(p->head_dim / 8);
+    const dim3 grid((row_chunks + pcpa::cache::kThreads - 1) / pcpa::cache::kThreads, p->num_kv_heads);
+    const dim3 block(pcpa::cache::kThreads);
+    const hipStream_t hs = (hipStream_t)stream;
+    if (fp8 && pow2)
+        hipLaunchKernelGGL((pcpa::cache::kv_write_kernel<true, true>), grid, block, 0, hs, a, row_chunks);
+    else if (fp8)
+        hipLaunchKernelGGL((pcpa::cache::kv_write_kernel<true, false>), grid, block, 0, hs, a, row_chunks);
+    else if (pow2)
+        hipLaunchKernelGGL((pcpa::cache::kv_write_kernel<false, true>), grid, block, 0, hs, a, row_chunks);
+    else
+        hipLaunchKernelGGL((pcpa::cache::kv_write_kernel<false, false>), grid, block, 0, hs, a, row_chunks);
+    return hipGetLastError() == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
 }
 
 }  // extern "C"

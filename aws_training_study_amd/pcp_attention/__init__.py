@@ -6,6 +6,7 @@ which in this repository is test infrastructure (``oracle/``), plus the
 kernel entry points and the paged-pool helpers.
 """
 
+from .cache import KVCacheWriter, absmax, build_page_pool
 from .config import PCPAttentionConfig, get_preset
 from .kernel import make_history_attention_kernel, pack_local_kv, wrap_for_native_torch
 from .layout import (
@@ -20,7 +21,10 @@ from .layout import (
 from .paging import make_block_table, pack_page_pool, page_valid_lengths, valid_lengths_from_block_mask
 
 __all__ = [
+    "KVCacheWriter",
     "PCPAttentionConfig",
+    "absmax",
+    "build_page_pool",
     "gather_history",
     "get_preset",
     "global_positions_for_rank",

@@ -99,20 +99,17 @@ class HistoryInputs:
 
 def _quantize_per_tensor(x: torch.Tensor) -> tuple[torch.Tensor, float]:
     values = x.float()
-    amax = float(values.abs().max())
-    scale = amax / FP8_E4M3_MAX if amax > 0 else 1.0
+    scale = per_tensor_scale(float(values.abs().max()))
     return (values / scale).to(torch.float8_e4m3fn), scale
 
 
-def make_scaled_inputs(
-    cfg: PCPAttentionConfig,
-    seed: int,
-    *,
-    kv_scale: str = "none",
-    k_prescale: str = "none",
-) -> HistoryInputs:
-    if kv_scale not in KV_SCALE_MODES:
-        raise ValueError(f"kv_scale must be one of {KV_SCALE_MODES}, got {kv_scale!r}")
+def make_raw_inputs(cfg: PCPAttentionConfig, seed: int, *, k_prescale: str = "none"):
+    """BF16 ``q [Hq, Q, D]``, ``k``/``v`` ``[Hkv, L, D]`` before any FP8 quantisation.
+
+    Same draws as ``make_scaled_inputs`` (and, without a pre-scale, as
+    ``make_inputs``) up to the storage cast; this is what a KV-cache producer
+    quantises.
+    """
     if k_prescale not in K_PRESCALE_MODES:
         raise ValueError(f"k_prescale must be one of {K_PRESCALE_MODES}, got {k_prescale!r}")
     generator = torch.Generator().manual_seed(seed)
@@ -126,6 +123,24 @@ def make_scaled_inputs(
         channel = torch.Generator().manual_seed(seed + 2)
         factor = torch.rand(cfg.num_kv_heads, 1, cfg.head_dim, generator=channel) * 1.5 + 0.5
         k = (k.float() * factor).to(torch.bfloat16)
+    return q, k, v
+
+
+def per_tensor_scale(amax: float) -> float:
+    """The per-tensor e4m3 scale for a tensor whose largest magnitude is ``amax``."""
+    return amax / FP8_E4M3_MAX if amax > 0 else 1.0
+
+
+def make_scaled_inputs(
+    cfg: PCPAttentionConfig,
+    seed: int,
+    *,
+    kv_scale: str = "none",
+    k_prescale: str = "none",
+) -> HistoryInputs:
+    if kv_scale not in KV_SCALE_MODES:
+        raise ValueError(f"kv_scale must be one of {KV_SCALE_MODES}, got {kv_scale!r}")
+    q, k, v = make_raw_inputs(cfg, seed, k_prescale=k_prescale)
     k_scale = v_scale = 1.0
     if cfg.kv_dtype == "fp8_e4m3fn":
         if kv_scale == "per_tensor":

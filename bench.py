@@ -45,6 +45,9 @@ def parse_args(argv=None):
     parser.add_argument("--steps", type=int, default=30)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--workload", default="full-fp8")
+    parser.add_argument("--path", choices=("history", "cache-write"), default="history",
+                        help="history: the attention launch (the headline metric); cache-write: the KV-cache "
+                             "producer filling the workload's page pool from BF16 K/V")
     parser.add_argument("--seed", type=int, default=1234)
     parser.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
                         help="approximate CPU time budget of the ring-model baseline sample")
@@ -134,6 +137,94 @@ def cpu_baseline(problem, budget_s: float) -> dict:
     }
 
 
+def cache_write_bench(args) -> int:
+    """KV-cache producer: quantise + scatter the workload's whole history into its page pool."""
+    import torch
+
+    from aws_training_study_amd.pcp_attention import KVCacheWriter, make_block_table, pack_page_pool, shard_history
+    from aws_training_study_amd.pcp_attention.cache import device_per_tensor_scale
+    from aws_training_study_amd.pcp_attention.inputs import make_raw_inputs, per_tensor_scale
+    from aws_training_study_amd.pcp_attention.workloads import get_workload
+
+    workload = get_workload(args.workload)
+    cfg = workload.resolve(args.seed).with_overrides(backend="hip")
+    if not cfg.is_history_aligned:
+        raise SystemExit("cache-write bench expects a block-aligned workload")
+    _, k, v = make_raw_inputs(cfg, args.seed)
+    table = make_block_table(cfg, args.seed + 1)
+    device = torch.device("cuda", 0)
+    kd, vd, td = k.to(device), v.to(device), table.to(device)
+    fp8 = cfg.kv_dtype == "fp8_e4m3fn"
+    ks = device_per_tensor_scale(kd) if fp8 else 1.0
+    vs = device_per_tensor_scale(vd) if fp8 else 1.0
+    dtype = torch.float8_e4m3fn if fp8 else torch.bfloat16
+    pool = torch.zeros((cfg.num_pages, cfg.page_elements), dtype=dtype, device=device)
+    writer = KVCacheWriter(cfg)
+
+    def step():
+        writer(kd, vd, pool, td, k_scale=ks, v_scale=vs)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(device)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for begin, end in events:
+        begin.record(stream)
+        step()
+        end.record(stream)
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    launch_ms = sorted(b.elapsed_time(e) for b, e in events)
+    elems = 2 * cfg.num_kv_heads * cfg.actual_history_len * cfg.head_dim
+    algo = elems * 2 + elems * (1 if fp8 else 2) + 4 * cfg.num_pages  # read bf16, write pages, table
+    ms_per_step = wall_s * 1e3 / args.steps
+    kernel_ms = statistics.fmean(launch_ms)
+    result = {
+        "metric": "KV-cache write GB/s (BF16 K/V -> paged pool, quantise + scatter), 1 GPU",
+        "value": round(algo / (ms_per_step * 1e-3) / 1e9, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3" if fp8 else "bf16",
+        "data": "synthetic (seeded N(0,1) BF16 K/V)",
+        "config": {"workload": workload.name, "tokens": cfg.actual_history_len, "kv_heads": cfg.num_kv_heads,
+                   "head_dim": cfg.head_dim, "pcp_ranks": cfg.pcp_size, "block_size": cfg.block_size,
+                   "interleave": cfg.interleave_size, "kv_dtype": cfg.kv_dtype},
+        "kernel_ms": {"min": round(launch_ms[0], 4), "median": round(statistics.median(launch_ms), 4),
+                      "mean": round(kernel_ms, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(algo / (kernel_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(algo / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "algorithmic_bytes": algo},
+    }
+    if not args.no_cpu_baseline:
+        threads = os.cpu_count() or 1
+        torch.set_num_threads(threads)
+        start = time.perf_counter()
+        if fp8:
+            kq = (k.float() / per_tensor_scale(float(k.float().abs().max()))).to(torch.float8_e4m3fn)
+            vq = (v.float() / per_tensor_scale(float(v.float().abs().max()))).to(torch.float8_e4m3fn)
+        else:
+            kq, vq = k, v
+        pack_page_pool(*shard_history(kq, vq, cfg), cfg, table)
+        host_s = time.perf_counter() - start
+        result["cpu_baseline"] = {
+            "value": round(algo / host_s / 1e9, 2), "unit": "GB/s", "ms": round(host_s * 1e3, 1), "cores": threads,
+            "kind": "port",
+            "sample": "host chain of the reference (quantise, shard_history, pack_local_kv, place by block table) "
+                      "over the whole history, torch CPU",
+        }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
@@ -148,6 +239,8 @@ def main(argv=None) -> int:
         return 2
     if args.copy_probe_mib:
         return copy_probe(args.copy_probe_mib, args.steps)
+    if args.path == "cache-write":
+        return cache_write_bench(args)
 
     import torch
 

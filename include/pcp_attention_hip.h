@@ -120,6 +120,38 @@ int32_t pcpa_history_attention(const pcpa_params* params, const void* q, const v
                                const int32_t* block_table, const int32_t* page_valid_len,
                                void* out, void* stream);
 
+/*
+ * KV-cache producer (the step before the attention): quantise K and V of the
+ * history tokens at global positions [first_pos, first_pos + num_tokens) and
+ * write them into their pages, in pack_local_kv's row format.  Replaces the
+ * host chain shard_history (layout.py:54-98) -> float8 cast (run_poc.py:
+ * 96-103, here with per-tensor scales) -> pack_local_kv (kernel.py:17-29) ->
+ * page placement by the block table, and also serves appends.
+ *   k, v        [num_kv_heads, num_tokens, head_dim] bf16 (global token order)
+ *   kv_pages    pool as for pcpa_history_attention (params.kv_dtype); only
+ *               the rows of the written tokens change
+ *   e4m3 pools store round_e4m3(x / params.k_scale) (v_scale for V), bit
+ *   for bit torch's (x.float() / scale).to(torch.float8_e4m3fn); bf16 pools
+ *   store x unchanged.  Token p belongs to rank (p / interleave) % pcp_size at
+ *   local position ((p / interleave) / pcp_size) * interleave + p % interleave
+ *   (layout.py:10-16), i.e. block local / block_size, slot local % block_size.
+ *   Tokens whose table entry is outside [0, num_pages) are not written.
+ *   page_valid_len (optional, int32 [pcp_size, max_local_blocks]): each
+ *   written token's entry is raised to at least slot + 1.
+ * The q/out fields of params are validated but unused.
+ */
+int32_t pcpa_kv_cache_write(const pcpa_params* params, int32_t interleave, int64_t first_pos,
+                            int32_t num_tokens, const void* k, const void* v,
+                            const int32_t* block_table, void* kv_pages, int32_t* page_valid_len,
+                            void* stream);
+
+/*
+ * max |x| over n bf16 values into *amax (device float): the amax of the
+ * per-tensor e4m3 scale amax / 448 (the FP8 configurations' K/V
+ * quantisation).  Two launches on `stream`; *amax needs no initialisation.
+ */
+int32_t pcpa_absmax_bf16(const void* x, int64_t n, float* amax, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -108,3 +108,24 @@ def test_python_entry_validates_before_launch():
     q = torch.zeros(4, 32, 64, 256, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="GPU tensor"):
         kernel(q, torch.zeros(4, 10), torch.zeros(4, 1, dtype=torch.int32))
+
+
+def test_cache_write_validates_without_a_gpu(lib):
+    """pcpa_kv_cache_write / pcpa_absmax_bf16 argument errors come back before any HIP call."""
+    p = _good_params()  # pcp 4, Hkv 2, D 64, block 128, 4 local blocks: 512 local slots per rank
+    w = lib.pcpa_kv_cache_write
+    assert w(None, 16, 0, 8, 16, 16, 16, 16, None, None) == -1
+    assert w(ctypes.byref(p), 16, 0, 8, None, 16, 16, 16, None, None) == -1
+    assert w(ctypes.byref(p), 16, 0, 8, 16, 16, None, 16, None, None) == -1
+    assert w(ctypes.byref(p), 0, 0, 8, 16, 16, 16, 16, None, None) == -3      # interleave
+    assert w(ctypes.byref(p), 16, -1, 8, 16, 16, 16, 16, None, None) == -3    # first_pos
+    assert w(ctypes.byref(p), 16, 0, -1, 16, 16, 16, 16, None, None) == -3    # num_tokens
+    assert w(ctypes.byref(p), 16, 0, 8, 8, 16, 16, 16, None, None) == -6      # k alignment
+    assert w(ctypes.byref(p), 16, 0, 8, 16, 16, 2, 16, None, None) == -6      # table alignment
+    assert w(ctypes.byref(p), 16, 0, 0, 16, 16, 16, 16, None, None) == 0      # nothing to write
+    # capacity: 4 ranks x 512 slots = global positions [0, 2048)
+    assert w(ctypes.byref(p), 16, 2040, 9, 16, 16, 16, 16, None, None) == -3
+    assert w(ctypes.byref(_good_params(head_dim=96)), 16, 0, 8, 16, 16, 16, 16, None, None) == -5
+    assert lib.pcpa_absmax_bf16(None, 8, 16, None) == -1
+    assert lib.pcpa_absmax_bf16(16, -1, 16, None) == -3
+    assert lib.pcpa_absmax_bf16(8, 8, 16, None) == -6

@@ -1,0 +1,161 @@
+"""GPU parity of the KV-cache producer (pcpa_kv_cache_write / pcpa_absmax_bf16).
+
+The reference's producer is the host chain shard_history (layout.py:54-98)
+-> float8 cast (run_poc.py:96-103) -> pack_local_kv (kernel.py:17-29); the
+host path here (shard_history + pack_page_pool, whose layout maps the CPU
+suite pins against the reference's tests) is the comparison, and torch's
+own float -> float8_e4m3fn cast is the quantisation reference.  Pools must
+be bit-identical.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from aws_training_study_amd.pcp_attention import (
+    KVCacheWriter,
+    PCPAttentionConfig,
+    absmax,
+    build_page_pool,
+    make_block_table,
+    make_history_attention_kernel,
+    pack_page_pool,
+    page_valid_lengths,
+    shard_history,
+    shard_history_bucket,
+)
+from aws_training_study_amd.pcp_attention.inputs import make_raw_inputs, per_tensor_scale
+
+pytestmark = pytest.mark.gpu
+
+CASES = {
+    # c2's shape (16 ranks, fp8, per-tensor scales)
+    "four-chip-fp8": dict(pcp_size=16, num_q_heads=32, num_kv_heads=2, head_dim=256, current_len=1024,
+                          max_history_len=8192, actual_history_len=8192, block_size=512, interleave_size=64,
+                          kv_dtype="fp8_e4m3fn"),
+    # c1's shape (bf16 pool: a plain scatter)
+    "tiny-bf16": dict(pcp_size=4, num_q_heads=8, num_kv_heads=2, head_dim=64, current_len=256,
+                      max_history_len=2048, actual_history_len=2048, block_size=128, interleave_size=16,
+                      kv_dtype="bfloat16"),
+    # 3 ranks, interleave 48, 192-token blocks: the general (non power of two) index maps
+    "odd-ranks-fp8": dict(pcp_size=3, num_q_heads=8, num_kv_heads=2, head_dim=64, current_len=144,
+                          max_history_len=1152, actual_history_len=1152, block_size=192, interleave_size=48,
+                          kv_dtype="fp8_e4m3fn"),
+    # unaligned runtime length stored at the bucket (c4-style), D=128
+    "bucket-fp8-d128": dict(pcp_size=8, num_q_heads=16, num_kv_heads=2, head_dim=128, current_len=512,
+                            max_history_len=8192, actual_history_len=5000, block_size=256, interleave_size=64,
+                            kv_dtype="fp8_e4m3fn"),
+}
+
+
+def _config(name):
+    return PCPAttentionConfig(**CASES[name], backend="hip").validate()
+
+
+def _host_pool(cfg, k, v, table):
+    """Reference-order host build: quantise per tensor, shard, pack, place."""
+    if cfg.kv_dtype == "fp8_e4m3fn":
+        ks = per_tensor_scale(float(k.float().abs().max()))
+        vs = per_tensor_scale(float(v.float().abs().max()))
+        kq = (k.float() / ks).to(torch.float8_e4m3fn)
+        vq = (v.float() / vs).to(torch.float8_e4m3fn)
+    else:
+        ks = vs = 1.0
+        kq, vq = k, v
+    shard = shard_history if cfg.is_history_aligned else shard_history_bucket
+    k_shards, v_shards = shard(kq, vq, cfg)
+    return pack_page_pool(k_shards, v_shards, cfg, table), ks, vs
+
+
+def _bytes(t):
+    return t.contiguous().view(torch.uint8) if t.element_size() == 1 else t.contiguous().view(torch.int16)
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_producer_pool_is_bit_identical_to_host_pool(name, cuda_device):
+    cfg = _config(name)
+    _, k, v = make_raw_inputs(cfg, seed=11)
+    table = make_block_table(cfg, seed=12)
+    host_pool, ks, vs = _host_pool(cfg, k, v, table)
+    print(f"{name}: writing {k.shape[1]} tokens x {cfg.num_kv_heads} heads", flush=True)
+    pool, gks, gvs, valid = build_page_pool(cfg, k.to(cuda_device), v.to(cuda_device), table)
+    torch.cuda.synchronize()
+    assert (gks, gvs) == (ks, vs), "device amax must give the host's scales exactly"
+    assert torch.equal(_bytes(pool).cpu(), _bytes(host_pool)), f"{name}: page pools differ"
+    # the valid lengths cover exactly the written tokens (the whole bucket when unaligned)
+    expect = page_valid_lengths(cfg.with_overrides(actual_history_len=k.shape[1]))
+    assert torch.equal(valid.cpu(), expect.to(torch.int32))
+
+
+def test_absmax_matches_torch(cuda_device):
+    gen = torch.Generator().manual_seed(5)
+    for n in (1, 7, 8, 1000, 4096 * 8 + 3, 1 << 20):
+        x = (torch.randn(n, generator=gen) * 3).to(torch.bfloat16)
+        x[n // 2] = -17.5
+        got = float(absmax(x.to(cuda_device)))
+        assert got == float(x.float().abs().max()), n
+
+
+def test_e4m3_codes_match_torch_cast(cuda_device):
+    """Round-to-nearest-even, the 448/464/480 boundary, subnormals, signed zeros,
+    infinities and NaN: the producer's codes equal torch's float8_e4m3fn cast."""
+    cfg = PCPAttentionConfig(pcp_size=1, num_q_heads=2, num_kv_heads=1, head_dim=64, current_len=64,
+                             max_history_len=64, actual_history_len=64, block_size=64, interleave_size=64,
+                             kv_dtype="fp8_e4m3fn", backend="hip").validate()
+    special = torch.tensor([0.0, -0.0, 1.0, 448.0, 449.0, 463.0, 464.0, 465.0, 480.0, 1e6, -1e6,
+                            float("inf"), float("-inf"), float("nan"), -float("nan"), 2.0 ** -6, 2.0 ** -7,
+                            2.0 ** -9, 2.0 ** -10, 2.0 ** -10 * 1.015625, 3 * 2.0 ** -10, 5 * 2.0 ** -10,
+                            1.0625, 1.1875, -2.3e-5, 0.0013], dtype=torch.float32)
+    gen = torch.Generator().manual_seed(3)
+    sweep = torch.randn(64 * 64 - special.numel(), generator=gen) * torch.exp2(torch.randint(-12, 10, (64 * 64 - special.numel(),),
+                                                                                               generator=gen).float())
+    x = torch.cat([special, sweep]).to(torch.bfloat16).reshape(1, 64, 64)
+    pool = torch.zeros((cfg.num_pages, cfg.page_elements), dtype=torch.float8_e4m3fn, device=cuda_device)
+    table = torch.arange(cfg.num_pages, dtype=torch.int32).reshape(1, -1).to(cuda_device)
+    for scale in (1.0, 0.37):
+        KVCacheWriter(cfg)(x.to(cuda_device), x.to(cuda_device), pool, table, k_scale=scale, v_scale=scale)
+        torch.cuda.synchronize()
+        expect = (x.float() / scale).to(torch.float8_e4m3fn).view(torch.uint8).reshape(-1)
+        got = pool.view(torch.uint8).cpu()[0, : 64 * 64]
+        mismatch = (got != expect).nonzero().flatten()
+        assert mismatch.numel() == 0, [(float(x.reshape(-1)[i]), int(got[i]), int(expect[i])) for i in mismatch[:8]]
+
+
+def test_appends_equal_one_write_and_track_valid_lengths(cuda_device):
+    cfg = _config("four-chip-fp8")
+    _, k, v = make_raw_inputs(cfg, seed=21)
+    table = make_block_table(cfg, seed=22).to(cuda_device)
+    kd, vd = k.to(cuda_device), v.to(cuda_device)
+    ks = per_tensor_scale(float(k.float().abs().max()))
+    vs = per_tensor_scale(float(v.float().abs().max()))
+    writer = KVCacheWriter(cfg)
+    one = torch.zeros((cfg.num_pages, cfg.page_elements), dtype=torch.float8_e4m3fn, device=cuda_device)
+    writer(kd, vd, one, table, k_scale=ks, v_scale=vs)
+    pieces = torch.zeros_like(one)
+    valid = torch.zeros((cfg.pcp_size, cfg.max_local_blocks), dtype=torch.int32, device=cuda_device)
+    cuts = [0, 1, 63, 64, 1000, 4097, 8192]
+    for start, stop in zip(cuts[:-1], cuts[1:]):
+        writer(kd[:, start:stop].contiguous(), vd[:, start:stop].contiguous(), pieces, table, first_pos=start,
+               k_scale=ks, v_scale=vs, page_valid_len=valid)
+        torch.cuda.synchronize()
+        expect = page_valid_lengths(cfg.with_overrides(actual_history_len=stop))
+        assert torch.equal(valid.cpu(), expect.to(torch.int32)), f"valid lengths after {stop} tokens"
+    assert torch.equal(one.view(torch.uint8), pieces.view(torch.uint8))
+
+
+def test_attention_on_producer_pool_matches_host_pool(cuda_device):
+    """End to end: the pool written on the GPU gives bit-identical attention output."""
+    cfg = _config("four-chip-fp8")
+    q, k, v = make_raw_inputs(cfg, seed=31)
+    table = make_block_table(cfg, seed=32)
+    host_pool, ks, vs = _host_pool(cfg, k, v, table)
+    pool, _, _, valid = build_page_pool(cfg, k.to(cuda_device), v.to(cuda_device), table)
+    from aws_training_study_amd.pcp_attention import stacked_query
+
+    qs = stacked_query(q, cfg).to(cuda_device)
+    kernel = make_history_attention_kernel(cfg)
+    a = kernel(qs, host_pool.to(cuda_device), table.to(cuda_device), page_valid_len=valid, k_scale=ks, v_scale=vs)
+    b = kernel(qs, pool, table.to(cuda_device), page_valid_len=valid, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
