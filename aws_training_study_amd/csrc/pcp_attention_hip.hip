@@ -1440,24 +1440,49 @@ __global__ void __launch_bounds__(kThreads) kv_write_kernel(WriteArgs a, uint32_
 // ordered like unsigned integers); *out is cleared first by init_kernel.
 __global__ void absmax_init_kernel(uint32_t* out) { *out = 0u; }
 
-__global__ void __launch_bounds__(kThreads) absmax_kernel(const uint16_t* x, int64_t n, uint32_t* out) {
-    float m = 0.f;
-    const int64_t stride = (int64_t)gridDim.x * kThreads * 8;
-    for (int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 8; i < n; i += stride) {
-        if (i + 8 <= n) {
+// Workgroup b reduces the contiguous span [b * span, (b + 1) * span) with
+// four 16-byte loads in flight per thread, then one atomic per workgroup.
+__global__ void __launch_bounds__(kThreads) absmax_kernel(const uint16_t* x, int64_t n, int64_t span,
+                                                          uint32_t* out) {
+    constexpr int kVec = 8, kUnroll = 4, kStep = kThreads * kVec;
+    __shared__ float partial[kThreads / 64];
+    const int64_t begin = (int64_t)blockIdx.x * span;
+    const int64_t end = begin + span < n ? begin + span : n;
+    float m[kUnroll] = {0.f, 0.f, 0.f, 0.f};
+    int64_t i = begin + threadIdx.x * kVec;
+    for (; i + (kUnroll - 1) * kStep + kVec <= end; i += kUnroll * kStep) {
+        v4i raw[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) raw[u] = *(const v4i*)(x + i + u * kStep);
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                m[u] = fmaxf(m[u], fabsf(bf16_bits_to_f32((uint32_t)raw[u][w] & 0xffffu)));
+                m[u] = fmaxf(m[u], fabsf(bf16_bits_to_f32((uint32_t)raw[u][w] >> 16)));
+            }
+    }
+    for (; i < end; i += kStep) {
+        if (i + kVec <= end) {
             const v4i raw = *(const v4i*)(x + i);
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                m = fmaxf(m, fabsf(bf16_bits_to_f32((uint32_t)raw[w] & 0xffffu)));
-                m = fmaxf(m, fabsf(bf16_bits_to_f32((uint32_t)raw[w] >> 16)));
+                m[0] = fmaxf(m[0], fabsf(bf16_bits_to_f32((uint32_t)raw[w] & 0xffffu)));
+                m[0] = fmaxf(m[0], fabsf(bf16_bits_to_f32((uint32_t)raw[w] >> 16)));
             }
         } else {
-            for (int64_t e = i; e < n; ++e) m = fmaxf(m, fabsf(bf16_bits_to_f32(x[e])));
+            for (int64_t e = i; e < end; ++e) m[0] = fmaxf(m[0], fabsf(bf16_bits_to_f32(x[e])));
         }
     }
+    float r = fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]));
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    if ((threadIdx.x & 63) == 0) atomicMax(out, __float_as_uint(m));
+    for (int off = 32; off >= 1; off >>= 1) r = fmaxf(r, __shfl_xor(r, off));
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = r;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kThreads / 64; ++w) r = fmaxf(r, partial[w]);
+        atomicMax(out, __float_as_uint(r));
+    }
 }
 
 }  // namespace cache
@@ -1580,10 +1605,14 @@ int32_t pcpa_absmax_bf16(const void* x, int64_t n, float* amax, void* stream) {
     hipLaunchKernelGGL(pcpa::cache::absmax_init_kernel, dim3(1), dim3(1), 0, st, (uint32_t*)amax);
     if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
     if (n == 0) return PCPA_OK;
-    const int64_t groups = (n + 8 * pcpa::cache::kThreads - 1) / (8 * pcpa::cache::kThreads);
-    const unsigned blocks = (unsigned)(groups < 2048 ? groups : 2048);
+    // spans of whole 8-element groups (the span start stays 16-byte aligned),
+    // at least 32 KB each, at most 2048 workgroups
+    constexpr int64_t kMinSpan = 16384;
+    int64_t span = (n + 2047) / 2048;
+    span = span < kMinSpan ? kMinSpan : (span + 7) / 8 * 8;
+    const unsigned blocks = (unsigned)((n + span - 1) / span);
     hipLaunchKernelGGL(pcpa::cache::absmax_kernel, dim3(blocks), dim3(pcpa::cache::kThreads), 0, st,
-                       (const uint16_t*)x, n, (uint32_t*)amax);
+                       (const uint16_t*)x, n, span, (uint32_t*)amax);
     return hipGetLastError() == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
 }
 

@@ -178,6 +178,7 @@ def cache_write_bench(args) -> int:
     torch.cuda.synchronize()
     wall_s = time.perf_counter() - t0
     launch_ms = sorted(b.elapsed_time(e) for b, e in events)
+    traffic, traffic_source = measured_traffic(f"{workload.name}/cache-write")
     elems = 2 * cfg.num_kv_heads * cfg.actual_history_len * cfg.head_dim
     algo = elems * 2 + elems * (1 if fp8 else 2) + 4 * cfg.num_pages  # read bf16, write pages, table
     ms_per_step = wall_s * 1e3 / args.steps
@@ -202,7 +203,7 @@ def cache_write_bench(args) -> int:
                       "mean": round(kernel_ms, 4)},
         "roofline": {"bound": "hbm", "achieved": round(algo / (kernel_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(algo / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None, "algorithmic_bytes": algo},
+                     "traffic": traffic, "traffic_source": traffic_source, "algorithmic_bytes": algo},
     }
     if not args.no_cpu_baseline:
         threads = os.cpu_count() or 1
