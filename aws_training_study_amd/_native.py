@@ -43,6 +43,8 @@ EXPORTED_SYMBOLS = (
     "pcpa_status_string",
     "pcpa_check_params",
     "pcpa_history_attention",
+    "pcpa_history_attention_lse",
+    "pcpa_current_attention",
     "pcpa_kv_cache_write",
     "pcpa_absmax_bf16",
 )
@@ -115,6 +117,10 @@ def load_library() -> ctypes.CDLL:
         ctypes.c_void_p,
         ctypes.c_void_p,
     ]
+    lib.pcpa_history_attention_lse.restype = ctypes.c_int32
+    lib.pcpa_history_attention_lse.argtypes = [ctypes.POINTER(PcpaParams)] + [ctypes.c_void_p] * 7
+    lib.pcpa_current_attention.restype = ctypes.c_int32
+    lib.pcpa_current_attention.argtypes = [ctypes.POINTER(PcpaParams), ctypes.c_int32] + [ctypes.c_void_p] * 7
     lib.pcpa_kv_cache_write.restype = ctypes.c_int32
     lib.pcpa_kv_cache_write.argtypes = [
         ctypes.POINTER(PcpaParams),

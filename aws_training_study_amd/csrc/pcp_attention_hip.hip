@@ -11,7 +11,7 @@
 //   * history_fwd_kernel<D, STORE8, FP8>: 4 waves x 32 rows per workgroup,
 //     two workgroups per CU, double-buffered tiles; every head dim (64, 128,
 //     256) and precision (e4m3 or bf16 MFMAs).
-//   * ovl::history_fwd_overlap<256, FAST>: the e4m3-MFMA path at head_dim 256,
+//   * ovl::history_fwd_overlap<256, FAST, LSE>: the e4m3-MFMA path at head_dim 256,
 //     8 waves x 32 rows, a two-stage in-wave pipeline with the two waves of a
 //     SIMD staggered by half a tile step (see its header).
 //
@@ -87,7 +87,19 @@ struct FwdArgs {
     int32_t block_size;
     float score_scale;     // softmax_scale * k_scale * log2(e)
     float v_scale;
+    float* lse;            // optional: natural-log sum of exp(score) per row, [pcp, Hq, local_q]
+    // Causal current-token attention only (history_fwd_kernel<..., CAUSAL>):
+    const uint8_t* merge_o;   // optional history output to merge with, bf16 like `out`
+    const float* merge_lse;   // its per-row log-sum-exp
+    int32_t interleave;       // striping of the current tokens over ranks
+    int32_t pcp;
 };
+
+// ln(E[(1 + f) / 2^f]) for f uniform in [0, 1): how much the linear-mantissa
+// exp2 of the FP8 overlap kernel overestimates a sum of exponentials on
+// average (1.04069); subtracted from that kernel's log-sum-exp outputs.
+constexpr float kFastLseBias = 0.03987f;
+constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
     return __uint_as_float(bits16 << 16);
@@ -229,6 +241,18 @@ __device__ __forceinline__ TileCursor next_tile(const FwdArgs& a, int head, Tile
     return TileCursor{a.num_entries, 0, 0, 0};
 }
 
+// The tile after `c` in the single "page" of the current tokens (CAUSAL
+// kernels): entry 0 holds all block_size current tokens in global order;
+// there is no block table.
+__device__ __forceinline__ TileCursor next_current_tile(const FwdArgs& a, int head, TileCursor c) {
+    if (c.e < 0) return TileCursor{0, 0, a.block_size, (int64_t)head * a.head_stride};
+    if (c.base + kKeyTile < c.n) {
+        c.base += kKeyTile;
+        return c;
+    }
+    return TileCursor{a.num_entries, 0, 0, 0};
+}
+
 // STORE8: the cache holds e4m3 (else bf16).  FP8: the MFMAs run on e4m3
 // operands (requires STORE8); otherwise they run on bf16, and an e4m3 cache
 // is widened to bf16 while it is staged into LDS.
@@ -363,7 +387,9 @@ using QOperand = typename std::conditional<S::ES == 1, v8i, v8bf>::type;
 
 // One 64-key tile held in LDS buffer BUF: S^T = K Q^T, masked online
 // softmax, O^T += V^T P^T.
-template <class S, int BUF>
+// CAUSAL: `valid` differs per lane (the row's causal limit within the tile,
+// possibly <= 0).
+template <class S, int BUF, bool CAUSAL = false>
 __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, const QOperand<S> (&qop)[S::QK],
                                              float cscale, const LaneMap<S>& L, int h, SoftmaxState<S>& st) {
     constexpr bool FP8 = S::ES == 1;
@@ -393,7 +419,8 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
     }
 
     // ---- mask, online softmax (lazy rescale) ----------------------------
-    if (valid < kKeyTile) {
+    // (CAUSAL: only tiles that cross some row's limit, a wave-uniform test)
+    if (CAUSAL ? __builtin_amdgcn_ballot_w64(valid < kKeyTile) != 0 : valid < kKeyTile) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -511,10 +538,11 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
 
 // Wait for tile `cur` (in BUF), start the prefetch of `nxt` into the other
 // buffer, then compute `cur`.
-template <class S, int BUF>
+template <class S, int BUF, bool CAUSAL>
 __device__ __forceinline__ void tile_step(const FwdArgs& a, const TileCursor& cur, const TileCursor& nxt,
                                           uint8_t* lds, int wave, int tid, int h, const LaneMap<S>& L,
-                                          const QOperand<S> (&qop)[S::QK], float cscale, SoftmaxState<S>& st) {
+                                          const QOperand<S> (&qop)[S::QK], float cscale, SoftmaxState<S>& st,
+                                          int row_limit) {
     const int valid = min(kKeyTile, cur.n - cur.base);
     uint8_t* const lds_v = lds + BUF * 2 * S::TILE + S::TILE;
     if constexpr (S::NBUF == 2) {
@@ -537,26 +565,44 @@ __device__ __forceinline__ void tile_step(const FwdArgs& a, const TileCursor& cu
         }
         __syncthreads();
     }
-    compute_tile<S, BUF>(lds, valid, qop, cscale, L, h, st);
+    compute_tile<S, BUF, CAUSAL>(lds, CAUSAL ? min(valid, row_limit - cur.base) : valid, qop, cscale, L, h, st);
 }
 
-template <int D, bool STORE8, bool FP8>
+// CAUSAL: causal attention of the current tokens among themselves (their
+// K/V are one page of block_size tokens in global order, no block table):
+// row (rank, token) sees current keys up to its own global position.  The
+// epilogue can then merge the result with a history output (merge_o,
+// merge_lse) by log-sum-exp.
+template <int D, bool STORE8, bool FP8, bool CAUSAL = false>
 __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_fwd_kernel(FwdArgs a) {
     using S = TileShape<D, STORE8, FP8>;
     constexpr int ROW = S::ROW, CHUNKS = S::CHUNKS, QK = S::QK, DT = S::DT;
 
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S::NBUF * 2 * S::TILE];
+    __shared__ int wave_limit[kWaves];
 
     // ---- XCD-aware work mapping ------------------------------------------
     // Workgroups are dealt to the 8 XCDs round-robin by launch index; give
     // each XCD a contiguous range of (KV head, row tile) work items so that
     // the workgroups sharing an XCD's L2 stream the same KV head together.
+    // CAUSAL: work grows with the row tile (later ranks see more current
+    // keys) and the keys fit in L2 anyway, so launch the heaviest tiles
+    // first, both heads alike, and let the early finishers take the light
+    // ones (longest-first balancing over all XCDs).
     const int items = a.row_tiles * a.num_kv_heads;
-    const int per_xcd = (items + 7) / 8;
-    const int item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-    if (item >= items) return;
-    const int head = item / a.row_tiles;
-    const int row_tile = item - head * a.row_tiles;
+    int head, row_tile;
+    if constexpr (CAUSAL) {
+        const int item = blockIdx.x;
+        if (item >= items) return;
+        head = item % a.num_kv_heads;
+        row_tile = a.row_tiles - 1 - item / a.num_kv_heads;
+    } else {
+        const int per_xcd = (items + 7) / 8;
+        const int item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+        if (item >= items) return;
+        head = item / a.row_tiles;
+        row_tile = item - head * a.row_tiles;
+    }
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -664,42 +710,88 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) st.o[dt] = v16f{};
 
-    TileCursor cur = next_tile(a, head, TileCursor{-1, 0, 0, 0});
+    // CAUSAL: the row sees current keys [0, g] (g its global current
+    // position, layout.py:10-16 inverted); the workgroup stops after the
+    // tile holding the largest g of its rows.
+    int row_limit = 0, group_limit = 0;
+    if constexpr (CAUSAL) {
+        row_limit = ((tok / a.interleave) * a.pcp + rank) * a.interleave + tok % a.interleave + 1;
+        int w = row_limit;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) w = max(w, __shfl_xor(w, off));
+        if (lane == 0) wave_limit[wave] = w;
+        __syncthreads();
+        group_limit = wave_limit[0];
+#pragma unroll
+        for (int i = 1; i < kWaves; ++i) group_limit = max(group_limit, wave_limit[i]);
+    }
+    auto advance = [&](const TileCursor& c) {
+        if constexpr (CAUSAL) {
+            const TileCursor n = next_current_tile(a, head, c);
+            return n.base < group_limit ? n : TileCursor{a.num_entries, 0, 0, 0};
+        } else {
+            return next_tile(a, head, c);
+        }
+    };
+
+    TileCursor cur = advance(TileCursor{-1, 0, 0, 0});
     if constexpr (S::NBUF == 2) {
         if (cur.e < a.num_entries) stage_tile_async<S, 0>(a, cur, lds, wave, L);
     }
     while (cur.e < a.num_entries) {
-        TileCursor nxt = next_tile(a, head, cur);
-        tile_step<S, 0>(a, cur, nxt, lds, wave, tid, h, L, qop, cscale, st);
+        TileCursor nxt = advance(cur);
+        tile_step<S, 0, CAUSAL>(a, cur, nxt, lds, wave, tid, h, L, qop, cscale, st, row_limit);
         cur = nxt;
         if constexpr (S::NBUF == 2) {
             if (cur.e >= a.num_entries) break;
-            nxt = next_tile(a, head, cur);
-            tile_step<S, 1>(a, cur, nxt, lds, wave, tid, h, L, qop, cscale, st);
+            nxt = advance(cur);
+            tile_step<S, 1, CAUSAL>(a, cur, nxt, lds, wave, tid, h, L, qop, cscale, st, row_limit);
             cur = nxt;
         }
     }
 
-    // ---- epilogue: O = O^T / l, bf16 ---------------------------------------
+    // ---- epilogue: O = O^T / l, bf16; log-sum-exp; merge -------------------
     const float l_tot = halves_sum(st.l);
-    const float scale = l_tot > 0.f ? a.v_scale / l_tot : 0.f;
+    float scale = l_tot > 0.f ? a.v_scale / l_tot : 0.f;
+    // sum_k exp(score_k) = l * 2^(m - bias): P was 2^(x - m + bias)
+    float lse = l_tot > 0.f ? __logf(l_tot) + (st.m - (FP8 ? kPBiasLog2 : 0.f)) * kLn2 : -INFINITY;
+    const int64_t row_index = row_off / (D * 2);
+    float hist_weight = 0.f;
+    if (CAUSAL && a.merge_o) {
+        // out = (e^lse_h O_h + e^lse O) / (e^lse_h + e^lse)
+        const float lse_h = a.merge_lse[row_index];
+        const float mx = fmaxf(lse_h, lse);
+        const float wh = lse_h == -INFINITY ? 0.f : __expf(lse_h - mx);
+        const float wc = __expf(lse - mx);
+        hist_weight = wh / (wh + wc);
+        scale *= wc / (wh + wc);
+        lse = mx + __logf(wh + wc);
+    }
     if (row_ok) {
         uint8_t* const orow = a.out + row_off;
+        const uint8_t* const hrow = CAUSAL && a.merge_o ? a.merge_o + row_off : nullptr;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
                 const int d = 32 * dt + 8 * r4 + 4 * h;
-                __bf16 v0 = (__bf16)(st.o[dt][4 * r4 + 0] * scale);
-                __bf16 v1 = (__bf16)(st.o[dt][4 * r4 + 1] * scale);
-                __bf16 v2 = (__bf16)(st.o[dt][4 * r4 + 2] * scale);
-                __bf16 v3 = (__bf16)(st.o[dt][4 * r4 + 3] * scale);
+                float o0 = st.o[dt][4 * r4 + 0] * scale, o1 = st.o[dt][4 * r4 + 1] * scale;
+                float o2 = st.o[dt][4 * r4 + 2] * scale, o3 = st.o[dt][4 * r4 + 3] * scale;
+                if (CAUSAL && hrow) {
+                    const v2i hv = *(const v2i*)(hrow + 2 * d);
+                    o0 = fmaf(hist_weight, bf16_bits_to_f32((uint32_t)hv[0] & 0xffffu), o0);
+                    o1 = fmaf(hist_weight, bf16_bits_to_f32((uint32_t)hv[0] >> 16), o1);
+                    o2 = fmaf(hist_weight, bf16_bits_to_f32((uint32_t)hv[1] & 0xffffu), o2);
+                    o3 = fmaf(hist_weight, bf16_bits_to_f32((uint32_t)hv[1] >> 16), o3);
+                }
+                const __bf16 v0 = (__bf16)o0, v1 = (__bf16)o1, v2 = (__bf16)o2, v3 = (__bf16)o3;
                 const uint32_t w0 = (uint32_t)__builtin_bit_cast(uint16_t, v0) |
                                     ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16);
                 const uint32_t w1 = (uint32_t)__builtin_bit_cast(uint16_t, v2) |
                                     ((uint32_t)__builtin_bit_cast(uint16_t, v3) << 16);
                 *(v2i*)(orow + 2 * d) = v2i{(int)w0, (int)w1};
             }
+        if (a.lse && h == 0) a.lse[row_index] = lse;
     }
 }
 
@@ -1147,7 +1239,9 @@ __device__ __forceinline__ void walk(const FwdArgs& a, uint8_t* lds, int wave, i
     }
 }
 
-template <int D, bool FAST>
+// LSE: also write each row's log-sum-exp (a separate instantiation, so that
+// the plain one keeps its register allocation).
+template <int D, bool FAST, bool LSE>
 __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     using S = Shape<D>;
     constexpr int QK = S::QK, DT = S::DT, ROW = S::ROW, CHUNKS = S::CHUNKS;
@@ -1271,8 +1365,14 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
             walk<D, true, FAST>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
     }
 
-    // ---- epilogue: O = O^T / l, bf16 -----------------------------------------
+    // ---- epilogue: O = O^T / l, bf16; log-sum-exp ---------------------------
     const float scale = sm.l > 0.f ? a.v_scale / sm.l : 0.f;
+    if (LSE && row_ok && h == 0) {
+        // sum_k exp(score_k) = l * 2^(m - 6), less the average overestimate
+        // of the linear-mantissa exp2
+        a.lse[row_off / (D * 2)] =
+            sm.l > 0.f ? __logf(sm.l) + (sm.m - kPBiasLog2) * kLn2 - (FAST ? kFastLseBias : 0.f) : -INFINITY;
+    }
     if (row_ok) {
         uint8_t* const orow = a.out + row_off;
 #pragma unroll
@@ -1488,6 +1588,25 @@ __global__ void __launch_bounds__(kThreads) absmax_kernel(const uint16_t* x, int
 }  // namespace cache
 }  // namespace pcpa
 
+namespace pcpa {
+
+// Launch arguments shared by every attention entry point (Q rows, output).
+inline FwdArgs common_args(const pcpa_params* p, const void* q, void* out) {
+    FwdArgs a{};
+    a.q = (const uint8_t*)q;
+    a.out = (uint8_t*)out;
+    a.group = p->num_q_heads / p->num_kv_heads;
+    a.group_rows = a.group * p->local_q_len;
+    a.rows_per_head = p->pcp_size * a.group_rows;
+    a.row_tiles = (a.rows_per_head + kRowsPerGroup - 1) / kRowsPerGroup;
+    a.local_q = p->local_q_len;
+    a.num_q_heads = p->num_q_heads;
+    a.num_kv_heads = p->num_kv_heads;
+    return a;
+}
+
+}  // namespace pcpa
+
 extern "C" {
 
 int32_t pcpa_abi_version(void) { return PCPA_ABI_VERSION; }
@@ -1533,49 +1652,43 @@ int32_t pcpa_check_params(const pcpa_params* p) {
     return PCPA_OK;
 }
 
-int32_t pcpa_history_attention(const pcpa_params* p, const void* q, const void* kv_pages,
-                               const int32_t* block_table, const int32_t* page_valid_len, void* out,
-                               void* stream) {
+int32_t pcpa_history_attention_lse(const pcpa_params* p, const void* q, const void* kv_pages,
+                                   const int32_t* block_table, const int32_t* page_valid_len, void* out,
+                                   float* lse, void* stream) {
     const int32_t st = pcpa_check_params(p);
     if (st != PCPA_OK) return st;
     if (!q || !kv_pages || !block_table || !page_valid_len || !out) return PCPA_ERR_NULL_POINTER;
     if (((uintptr_t)q | (uintptr_t)kv_pages | (uintptr_t)out) & 15u) return PCPA_ERR_MISALIGNED;
-    if (((uintptr_t)block_table | (uintptr_t)page_valid_len) & 3u) return PCPA_ERR_MISALIGNED;
+    if (((uintptr_t)block_table | (uintptr_t)page_valid_len | (uintptr_t)lse) & 3u) return PCPA_ERR_MISALIGNED;
 
     const bool store8 = p->kv_dtype == PCPA_DTYPE_FP8_E4M3FN;
     const bool fp8 = store8 && !(p->flags & PCPA_FLAG_BF16_MFMA);
     const int64_t es = store8 ? 1 : 2;
-    pcpa::FwdArgs a;
-    a.q = (const uint8_t*)q;
+    pcpa::FwdArgs a = pcpa::common_args(p, q, out);
     a.kv = (const uint8_t*)kv_pages;
     a.block_table = block_table;
     a.page_valid_len = page_valid_len;
-    a.out = (uint8_t*)out;
     a.head_stride = (int64_t)p->block_size * p->head_dim * es;
     a.page_stride = 2 * (int64_t)p->num_kv_heads * a.head_stride;
-    a.group = p->num_q_heads / p->num_kv_heads;
-    a.group_rows = a.group * p->local_q_len;
-    a.rows_per_head = p->pcp_size * a.group_rows;
-    a.local_q = p->local_q_len;
-    a.num_q_heads = p->num_q_heads;
-    a.num_kv_heads = p->num_kv_heads;
     a.num_entries = p->pcp_size * p->max_local_blocks;
     a.num_pages = p->num_pages;
     a.block_size = p->block_size;
     a.score_scale = p->softmax_scale * p->k_scale * pcpa::kLog2e;
     a.v_scale = p->v_scale;
+    a.lse = lse;
 
-    a.row_tiles = (a.rows_per_head + pcpa::kRowsPerGroup - 1) / pcpa::kRowsPerGroup;
-    const int items = a.row_tiles * p->num_kv_heads;
-    const dim3 grid(8 * ((items + 7) / 8));
-    const dim3 block(pcpa::kThreads);
     void* args[] = {&a};
     const void* fn = nullptr;
     if (fp8 && p->head_dim == 256) {
         a.row_tiles = (a.rows_per_head + pcpa::ovl::kRowsPerGroup - 1) / pcpa::ovl::kRowsPerGroup;
         const int oitems = a.row_tiles * p->num_kv_heads;
-        fn = (p->flags & PCPA_FLAG_EXACT_EXP2) ? (const void*)pcpa::ovl::history_fwd_overlap<256, false>
-                                               : (const void*)pcpa::ovl::history_fwd_overlap<256, true>;
+        const bool exact = p->flags & PCPA_FLAG_EXACT_EXP2;
+        if (lse)
+            fn = exact ? (const void*)pcpa::ovl::history_fwd_overlap<256, false, true>
+                       : (const void*)pcpa::ovl::history_fwd_overlap<256, true, true>;
+        else
+            fn = exact ? (const void*)pcpa::ovl::history_fwd_overlap<256, false, false>
+                       : (const void*)pcpa::ovl::history_fwd_overlap<256, true, false>;
         const hipError_t oerr = hipLaunchKernel(fn, dim3(8 * ((oitems + 7) / 8)), dim3(pcpa::ovl::kThreads), args, 0,
                                                 (hipStream_t)stream);
         return oerr == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
@@ -1592,10 +1705,61 @@ int32_t pcpa_history_attention(const pcpa_params* p, const void* q, const void* 
         case 256 * 4: fn = (const void*)pcpa::history_fwd_kernel<256, false, false>; break;
         default: return PCPA_ERR_UNSUPPORTED;
     }
-    const hipError_t err = hipLaunchKernel(fn, grid, block, args, 0, (hipStream_t)stream);
+    const int items = a.row_tiles * p->num_kv_heads;
+    const hipError_t err =
+        hipLaunchKernel(fn, dim3(8 * ((items + 7) / 8)), dim3(pcpa::kThreads), args, 0, (hipStream_t)stream);
     return err == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
 }
 
+int32_t pcpa_history_attention(const pcpa_params* p, const void* q, const void* kv_pages,
+                               const int32_t* block_table, const int32_t* page_valid_len, void* out,
+                               void* stream) {
+    return pcpa_history_attention_lse(p, q, kv_pages, block_table, page_valid_len, out, nullptr, stream);
+}
+
+int32_t pcpa_current_attention(const pcpa_params* p, int32_t interleave, const void* q, const void* kv_current,
+                               const void* hist_out, const float* hist_lse, void* out, float* lse,
+                               void* stream) {
+    const int32_t st = pcpa_check_params(p);
+    if (st != PCPA_OK) return st;
+    if (!q || !kv_current || !out) return PCPA_ERR_NULL_POINTER;
+    if ((hist_out == nullptr) != (hist_lse == nullptr)) return PCPA_ERR_NULL_POINTER;
+    if (p->kv_dtype != PCPA_DTYPE_BF16) return PCPA_ERR_BAD_DTYPE;
+    if (interleave <= 0 || p->local_q_len % interleave) return PCPA_ERR_BAD_SHAPE;
+    const int64_t current = (int64_t)p->pcp_size * p->local_q_len;
+    if (current % pcpa::kKeyTile) return PCPA_ERR_UNSUPPORTED;
+    if (((uintptr_t)q | (uintptr_t)kv_current | (uintptr_t)out | (uintptr_t)hist_out) & 15u)
+        return PCPA_ERR_MISALIGNED;
+    if (((uintptr_t)hist_lse | (uintptr_t)lse) & 3u) return PCPA_ERR_MISALIGNED;
+
+    pcpa::FwdArgs a = pcpa::common_args(p, q, out);
+    a.kv = (const uint8_t*)kv_current;
+    a.head_stride = current * p->head_dim * 2;
+    a.page_stride = 2 * (int64_t)p->num_kv_heads * a.head_stride;
+    a.num_entries = 1;
+    a.num_pages = 1;
+    a.block_size = (int32_t)current;
+    a.score_scale = p->softmax_scale * pcpa::kLog2e;  // BF16 current K/V: no dequantisation scale
+    a.v_scale = 1.f;
+    a.lse = lse;
+    a.merge_o = (const uint8_t*)hist_out;
+    a.merge_lse = hist_lse;
+    a.interleave = interleave;
+    a.pcp = p->pcp_size;
+
+    void* args[] = {&a};
+    const void* fn = nullptr;
+    switch (p->head_dim) {
+        case 64: fn = (const void*)pcpa::history_fwd_kernel<64, false, false, true>; break;
+        case 128: fn = (const void*)pcpa::history_fwd_kernel<128, false, false, true>; break;
+        case 256: fn = (const void*)pcpa::history_fwd_kernel<256, false, false, true>; break;
+        default: return PCPA_ERR_UNSUPPORTED;
+    }
+    const int items = a.row_tiles * p->num_kv_heads;
+    const hipError_t err =
+        hipLaunchKernel(fn, dim3(8 * ((items + 7) / 8)), dim3(pcpa::kThreads), args, 0, (hipStream_t)stream);
+    return err == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
+}
 
 int32_t pcpa_absmax_bf16(const void* x, int64_t n, float* amax, void* stream) {
     if (!x || !amax) return PCPA_ERR_NULL_POINTER;

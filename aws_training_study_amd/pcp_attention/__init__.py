@@ -3,11 +3,13 @@
 Same exported names as ``pcp_attention/__init__.py`` of the Trainium2 proof
 of concept (``__init__.py:3-15``) minus the CPU executable specification,
 which in this repository is test infrastructure (``oracle/``), plus the
-kernel entry points and the paged-pool helpers.
+kernel entry points, the paged-pool helpers, the KV-cache producer and the
+current-token step.
 """
 
 from .cache import KVCacheWriter, absmax, build_page_pool
 from .config import PCPAttentionConfig, get_preset
+from .current import CurrentAttentionKernel, PrefillAttention, stack_current_kv
 from .kernel import make_history_attention_kernel, pack_local_kv, wrap_for_native_torch
 from .layout import (
     gather_history,
@@ -21,6 +23,7 @@ from .layout import (
 from .paging import make_block_table, pack_page_pool, page_valid_lengths, valid_lengths_from_block_mask
 
 __all__ = [
+    "CurrentAttentionKernel",
     "KVCacheWriter",
     "PCPAttentionConfig",
     "absmax",
@@ -34,9 +37,11 @@ __all__ = [
     "pack_local_kv",
     "pack_page_pool",
     "page_valid_lengths",
+    "PrefillAttention",
     "shard_history",
     "shard_history_bucket",
     "shard_query",
+    "stack_current_kv",
     "stacked_query",
     "valid_lengths_from_block_mask",
     "wrap_for_native_torch",

@@ -86,6 +86,12 @@ class HistoryAttentionKernel:
       normalisation); ``"exact"`` rounds ``v_exp_f32``.  Other paths always
       use ``v_exp_f32``.
 
+    * ``return_lse``: also return each row's log-sum-exp (float32
+      ``[pcp, Hq, local_q]``, natural log of the sum of ``exp(score)`` over
+      the valid history keys, ``-inf`` for none) - the input of a merge with
+      the current tokens (``current.CurrentAttentionKernel``).  The call then
+      returns ``(out, lse)``.
+
     The launch is asynchronous on the current torch stream.
     """
 
@@ -149,6 +155,7 @@ class HistoryAttentionKernel:
         out=None,
         precision: str = "auto",
         exp2: str = "fast",
+        return_lse: bool = False,
     ):
         import torch
 
@@ -196,6 +203,9 @@ class HistoryAttentionKernel:
             out = torch.empty(q_shape, dtype=torch.bfloat16, device=device)
         elif tuple(out.shape) != q_shape or out.dtype != torch.bfloat16 or not out.is_contiguous() or out.device != device:
             raise ValueError(f"out must be contiguous bfloat16 {q_shape} on {device}")
+        lse = None
+        if return_lse:
+            lse = torch.empty(q_shape[:3], dtype=torch.float32, device=device)
         params = self._params(num_pages, k_scale, v_scale)
         if self.uses_bf16_mfma(precision):
             params.flags |= self._native.FLAG_BF16_MFMA
@@ -203,17 +213,18 @@ class HistoryAttentionKernel:
             params.flags |= self._native.FLAG_EXACT_EXP2
         with torch.cuda.device(device):
             stream = torch.cuda.current_stream(device).cuda_stream
-            status = self._lib.pcpa_history_attention(
+            status = self._lib.pcpa_history_attention_lse(
                 ctypes.byref(params),
                 q.data_ptr(),
                 kv_pages.data_ptr(),
                 block_table.data_ptr(),
                 page_valid_len.data_ptr(),
                 out.data_ptr(),
+                None if lse is None else lse.data_ptr(),
                 stream,
             )
         self._native.check(status)
-        return out
+        return (out, lse) if return_lse else out
 
 
 def make_history_attention_kernel(config: PCPAttentionConfig) -> HistoryAttentionKernel:

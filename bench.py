@@ -45,9 +45,10 @@ def parse_args(argv=None):
     parser.add_argument("--steps", type=int, default=30)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--workload", default="full-fp8")
-    parser.add_argument("--path", choices=("history", "cache-write"), default="history",
+    parser.add_argument("--path", choices=("history", "cache-write", "current"), default="history",
                         help="history: the attention launch (the headline metric); cache-write: the KV-cache "
-                             "producer filling the workload's page pool from BF16 K/V")
+                             "producer filling the workload's page pool from BF16 K/V; current: causal attention "
+                             "of the current tokens merged with the history output")
     parser.add_argument("--seed", type=int, default=1234)
     parser.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
                         help="approximate CPU time budget of the ring-model baseline sample")
@@ -226,6 +227,119 @@ def cache_write_bench(args) -> int:
     return 0
 
 
+def causal_flops(cfg) -> float:
+    """4 * D per (query, visible key) pair; query g sees current keys 0..g."""
+    return 2.0 * cfg.num_q_heads * cfg.head_dim * cfg.current_len * (cfg.current_len + 1)
+
+
+def _timed(step, steps, stream):
+    import torch
+
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for begin, end in events:
+        begin.record(stream)
+        step()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, sorted(b.elapsed_time(e) for b, e in events)
+
+
+def current_bench(args) -> int:
+    """Current-token step: causal attention among the current tokens, merged with a history result."""
+    import torch
+
+    from aws_training_study_amd.pcp_attention import CurrentAttentionKernel, PrefillAttention, stack_current_kv
+    from aws_training_study_amd.pcp_attention.workloads import build_workload_problem, get_workload
+
+    workload = get_workload(args.workload)
+    problem = build_workload_problem(workload, args.seed)
+    cfg = problem.config
+    device = torch.device("cuda", 0)
+    gpu = problem.to(device)
+    g = torch.Generator().manual_seed(args.seed + 11)
+    kv_shape = (cfg.num_kv_heads, cfg.current_len, cfg.head_dim)
+    kc = torch.randn(kv_shape, generator=g, dtype=torch.bfloat16)
+    vc = torch.randn(kv_shape, generator=g, dtype=torch.bfloat16)
+    kv_cur = stack_current_kv(kc, vc).to(device)
+    prefill = PrefillAttention(cfg)
+    current = prefill.current
+    hist_out, hist_lse = prefill.history(gpu.q_stacked, gpu.kv_pages, gpu.block_table,
+                                         page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale,
+                                         v_scale=problem.v_scale, return_lse=True)
+    out = torch.empty_like(hist_out)
+
+    def step():
+        current(gpu.q_stacked, kv_cur, hist_out, hist_lse, out=out)
+
+    for _ in range(args.warmup):
+        step()
+    stream = torch.cuda.current_stream(device)
+    wall_s, launch_ms = _timed(step, args.steps, stream)
+
+    def prefill_step():
+        prefill(gpu.q_stacked, gpu.kv_pages, gpu.block_table, kv_cur, page_valid_len=gpu.page_valid_len,
+                k_scale=problem.k_scale, v_scale=problem.v_scale)
+
+    prefill_step()
+    _, prefill_ms = _timed(prefill_step, max(3, min(args.steps, 10)), stream)
+
+    flops = causal_flops(cfg)
+    ms_per_step = wall_s * 1e3 / args.steps
+    kernel_ms = statistics.fmean(launch_ms)
+    achieved = flops / (kernel_ms * 1e-3) / 1e12
+    peak = PEAK_TFLOPS["bfloat16"]
+    history_flops = model_flops(cfg)
+    result = {
+        "metric": "current-token causal attention + LSE merge TFLOP/s (BF16 MFMA), 1 GPU",
+        "value": round(flops / (ms_per_step * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) BF16 Q and current K/V; history as the history bench)",
+        "config": {"workload": workload.name, "pcp_ranks": cfg.pcp_size, "current_tokens": cfg.current_len,
+                   "history_tokens": cfg.actual_history_len, "q_heads": cfg.num_q_heads,
+                   "kv_heads": cfg.num_kv_heads, "head_dim": cfg.head_dim, "interleave": cfg.interleave_size},
+        "kernel_ms": {"min": round(launch_ms[0], 4), "median": round(statistics.median(launch_ms), 4),
+                      "mean": round(kernel_ms, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(achieved / peak, 4), "traffic": None,
+                     "algorithmic_bytes": 2.0 * (3 * cfg.num_q_heads * cfg.current_len * cfg.head_dim
+                                                 + 2 * cfg.num_kv_heads * cfg.current_len * cfg.head_dim)
+                     + 2 * 4.0 * cfg.num_q_heads * cfg.current_len},
+        "prefill": {"ms_median": round(statistics.median(prefill_ms), 4),
+                    "tflops": round((history_flops + flops) / (statistics.median(prefill_ms) * 1e-3) / 1e12, 2),
+                    "what": "history attention with lse + this step, in place"},
+    }
+    if not args.no_cpu_baseline:
+        import torch.nn.functional as F
+
+        threads = os.cpu_count() or 1
+        torch.set_num_threads(threads)
+        group = cfg.num_q_heads // cfg.num_kv_heads
+        q = problem.inputs.q.float()
+        kk = kc.float().repeat_interleave(group, dim=0)
+        vv = vc.float().repeat_interleave(group, dim=0)
+        start = time.perf_counter()
+        F.scaled_dot_product_attention(q, kk, vv, is_causal=True, scale=cfg.softmax_scale)
+        host_s = time.perf_counter() - start
+        result["cpu_baseline"] = {
+            "value": round(flops / host_s / 1e12, 4), "unit": "TFLOP/s", "ms": round(host_s * 1e3, 1),
+            "cores": threads, "kind": "port",
+            "sample": "the whole workload's causal current attention (no merge): torch float32 "
+                      "scaled_dot_product_attention(is_causal=True) on the host",
+        }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
@@ -242,6 +356,8 @@ def main(argv=None) -> int:
         return copy_probe(args.copy_probe_mib, args.steps)
     if args.path == "cache-write":
         return cache_write_bench(args)
+    if args.path == "current":
+        return current_bench(args)
 
     import torch
 

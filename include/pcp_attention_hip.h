@@ -121,6 +121,51 @@ int32_t pcpa_history_attention(const pcpa_params* params, const void* q, const v
                                void* out, void* stream);
 
 /*
+ * pcpa_history_attention that also writes each row's log-sum-exp:
+ *   lse  [pcp_size, num_q_heads, local_q_len] float (optional, NULL = none):
+ *        natural log of sum_k exp(score_k) over the row's valid history
+ *        keys (scores as above), -INFINITY for a row with no valid key.
+ * This is what a later merge with other keys (the current tokens) needs.
+ * The e4m3 path at head_dim 256 without PCPA_FLAG_EXACT_EXP2 corrects the
+ * mean bias of its linear-mantissa exp2 (sum inflated by 1.0407 on average,
+ * i.e. lse - 0.0399); its lse is good to about 1e-3 over long histories.
+ * No reference counterpart: the reference kernel returns the normalised
+ * output only (kernel.py:546-551).
+ */
+int32_t pcpa_history_attention_lse(const pcpa_params* params, const void* q, const void* kv_pages,
+                                   const int32_t* block_table, const int32_t* page_valid_len,
+                                   void* out, float* lse, void* stream);
+
+/*
+ * Causal attention of the current tokens among themselves, optionally merged
+ * with a history result: the step after the history attention.  The
+ * reference stops at history-only attention ("current tokens do not attend
+ * to each other yet", README.md:17-18); the semantics here are the standard
+ * ones: the query at global current position g sees current keys 0..g.
+ *   q           [pcp_size, num_q_heads, local_q_len, head_dim] bf16, striped
+ *               as for pcpa_history_attention with `interleave` (the local
+ *               token t of rank r is global position
+ *               ((t / il) * pcp_size + r) * il + t % il, layout.py:10-16)
+ *   kv_current  [2, num_kv_heads, pcp_size * local_q_len, head_dim] bf16:
+ *               K then V of the current tokens in global order (one "page"
+ *               of block size pcp_size * local_q_len, which must be a
+ *               multiple of 64)
+ *   hist_out, hist_lse (optional, both or neither): the history output and
+ *               log-sum-exp of pcpa_history_attention_lse for the same q.
+ *               With them, out = softmax attention over history keys and
+ *               causal current keys together (log-sum-exp merge), and lse
+ *               covers both.
+ *   out         as q; may alias hist_out (each row is read before written)
+ *   lse         optional, as for pcpa_history_attention_lse
+ * params: kv_dtype must be bf16 here (current K/V are not quantised),
+ * k_scale / v_scale / block_size / max_local_blocks / num_pages are unused
+ * (validated only).
+ */
+int32_t pcpa_current_attention(const pcpa_params* params, int32_t interleave, const void* q,
+                               const void* kv_current, const void* hist_out, const float* hist_lse,
+                               void* out, float* lse, void* stream);
+
+/*
  * KV-cache producer (the step before the attention): quantise K and V of the
  * history tokens at global positions [first_pos, first_pos + num_tokens) and
  * write them into their pages, in pack_local_kv's row format.  Replaces the

@@ -20,6 +20,14 @@ pinned (tests/test_oracle.py):
   visited (rank, block, source rank) sequence.
 * per-rank valid length for unaligned histories - brute force over global
   positions with owner_and_local_position.
+* attention with log-sum-exp and per-row key limits (current-token causal
+  attention, merged with the history) - the lse against a per-row
+  ``math.fsum`` loop and the closed form ``c + ln n`` of n identical scores;
+  the causal and history-plus-current outputs against torch's
+  ``scaled_dot_product_attention`` (float64, is_causal / an explicit boolean
+  mask over the concatenated keys) on global-order queries, which also pins
+  the inverse of the striping.  The reference has no current-token
+  attention (README.md:17-18): these follow the standard causal definition.
 """
 
 from __future__ import annotations
@@ -342,6 +350,80 @@ def ring_history_attention(q_shards, k_shards, v_shards, shape: OracleShape, tra
                     m[qh] = m_new
         outputs.append(acc / l)
     return outputs
+
+
+def attention_with_lse(
+    q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, key_limit: np.ndarray | None = None
+) -> tuple[np.ndarray, np.ndarray]:
+    """float64 GQA attention (reference.py:16-32) plus each row's log-sum-exp.
+
+    ``q`` ``[Hq, M, D]``, ``k``/``v`` ``[Hkv, L, D]``; ``key_limit``
+    (optional, ``[M]``) lets query row i see keys ``[0, key_limit[i])`` only
+    (every head alike).  Returns ``out [Hq, M, D]`` and
+    ``lse [Hq, M] = ln sum_k exp(score_k)``; a row with no key gets a zero
+    output and ``-inf``.
+    """
+    hq, m, d = q.shape
+    hkv, length, _ = k.shape
+    if hq % hkv or v.shape != k.shape or k.shape[2] != d:
+        raise ValueError("incompatible Q/K/V shapes for grouped-query attention")
+    group = hq // hkv
+    out = np.zeros((hq, m, d), dtype=np.float64)
+    lse = np.full((hq, m), -np.inf, dtype=np.float64)
+    visible = None
+    if key_limit is not None:
+        visible = np.arange(length)[None, :] < np.asarray(key_limit, dtype=np.int64)[:, None]
+    for g in range(hkv):
+        kg = k[g].astype(np.float64)
+        vg = v[g].astype(np.float64)
+        for qh in range(g * group, (g + 1) * group):
+            s = q[qh].astype(np.float64) @ kg.T * scale
+            if visible is not None:
+                s = np.where(visible, s, -np.inf)
+            mx = s.max(axis=1, keepdims=True)
+            has = np.isfinite(mx[:, 0])
+            mx = np.where(np.isfinite(mx), mx, 0.0)
+            e = np.exp(s - mx)
+            total = e.sum(axis=1)
+            out[qh, has] = (e @ vg)[has] / total[has, None]
+            lse[qh, has] = mx[has, 0] + np.log(total[has])
+    return out, lse
+
+
+def current_positions(shape: OracleShape) -> np.ndarray:
+    """``[pcp, local_q]`` global current position of each rank's local token (layout.py:19-31)."""
+    return np.stack(
+        [global_positions(shape.current_len, r, shape.pcp_size, shape.interleave_size) for r in range(shape.pcp_size)]
+    )
+
+
+def expected_with_current(
+    q_global: np.ndarray,
+    k_cur: np.ndarray,
+    v_cur: np.ndarray,
+    shape: OracleShape,
+    k_hist: np.ndarray | None = None,
+    v_hist: np.ndarray | None = None,
+) -> tuple[np.ndarray, np.ndarray]:
+    """float64 ``(out, lse)`` ``[pcp, Hq, local_q, (D)]`` with current-token causal attention.
+
+    The query at global current position g sees the current keys ``0..g``
+    (``k_cur``/``v_cur`` ``[Hkv, current_len, D]`` in global order) and, when
+    ``k_hist`` is given, every history key ``< actual_history_len`` too.
+    """
+    positions = current_positions(shape)
+    length = shape.actual_history_len if k_hist is not None else 0
+    if k_hist is not None:
+        k = np.concatenate([k_hist[:, :length], k_cur], axis=1)
+        v = np.concatenate([v_hist[:, :length], v_cur], axis=1)
+    else:
+        k, v = k_cur, v_cur
+    outs, lses = [], []
+    for r, qs in enumerate(shard_query(q_global, shape)):
+        o, l = attention_with_lse(qs, k, v, shape.softmax_scale, key_limit=length + positions[r] + 1)
+        outs.append(o)
+        lses.append(l)
+    return np.stack(outs), np.stack(lses)
 
 
 def max_abs_and_mean_abs(actual: np.ndarray, expected: np.ndarray) -> tuple[float, float]:

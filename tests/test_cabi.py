@@ -129,3 +129,25 @@ def test_cache_write_validates_without_a_gpu(lib):
     assert lib.pcpa_absmax_bf16(None, 8, 16, None) == -1
     assert lib.pcpa_absmax_bf16(16, -1, 16, None) == -3
     assert lib.pcpa_absmax_bf16(8, 8, 16, None) == -6
+
+
+def test_lse_and_current_entries_validate_without_a_gpu(lib):
+    """pcpa_history_attention_lse / pcpa_current_attention argument errors come back before any HIP call."""
+    p = _good_params()  # pcp 4 x local_q 64 = 256 current tokens
+    h = lib.pcpa_history_attention_lse
+    assert h(None, 16, 16, 16, 16, 16, None, None) == -1
+    assert h(ctypes.byref(p), 16, 16, 16, 16, 16, 2, None) == -6       # lse alignment
+    assert h(ctypes.byref(_good_params(head_dim=96)), 16, 16, 16, 16, 16, None, None) == -5
+    c = lib.pcpa_current_attention
+    assert c(None, 16, 16, 16, None, None, 16, None, None) == -1
+    assert c(ctypes.byref(p), 16, None, 16, None, None, 16, None, None) == -1   # q
+    assert c(ctypes.byref(p), 16, 16, None, None, None, 16, None, None) == -1   # kv_current
+    assert c(ctypes.byref(p), 16, 16, 16, 16, None, 16, None, None) == -1       # hist_out without hist_lse
+    assert c(ctypes.byref(p), 16, 16, 16, None, 16, 16, None, None) == -1       # hist_lse without hist_out
+    assert c(ctypes.byref(_good_params(kv_dtype=2)), 16, 16, 16, None, None, 16, None, None) == -4
+    assert c(ctypes.byref(p), 0, 16, 16, None, None, 16, None, None) == -3      # interleave
+    assert c(ctypes.byref(p), 48, 16, 16, None, None, 16, None, None) == -3     # local_q % interleave
+    assert c(ctypes.byref(_good_params(local_q_len=8)), 8, 16, 16, None, None, 16, None, None) == -5  # 32 tokens
+    assert c(ctypes.byref(p), 16, 8, 16, None, None, 16, None, None) == -6      # q alignment
+    assert c(ctypes.byref(p), 16, 16, 16, 16, 2, 16, None, None) == -6          # hist_lse alignment
+    assert c(ctypes.byref(p), 16, 16, 16, None, None, 16, 2, None) == -6        # lse alignment

@@ -1,0 +1,209 @@
+"""GPU parity of the current-token step: history log-sum-exp, causal
+attention among the current tokens, and its log-sum-exp merge with the
+history output, against the float64 oracle.
+
+Bars: outputs max-abs <= 2e-2 and mean-abs <= 2e-3 (as for the history
+attention).  Log-sum-exp (natural log): e4m3 MFMA paths max-abs <= 5e-2,
+mean-abs <= 1e-2 - rounding Q to e4m3 alone moves the lse of the 16-rank
+FP8 workload by up to 1.2e-2 (mean 2.2e-3) against the exact Q; BF16 MFMA
+paths max-abs <= 5e-3, mean-abs <= 5e-4.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from aws_training_study_amd.pcp_attention import (
+    CurrentAttentionKernel,
+    PrefillAttention,
+    make_history_attention_kernel,
+    stack_current_kv,
+)
+from aws_training_study_amd.pcp_attention.config import PCPAttentionConfig
+from aws_training_study_amd.pcp_attention.workloads import build_paged_problem, build_workload_problem
+from oracle import pcp_oracle as orc
+
+from test_gpu_parity import _assert_close, _real_history, _sample_rows
+
+pytestmark = pytest.mark.gpu
+
+LSE_TOL = {"fp8": (5e-2, 1e-2), "bf16": (5e-3, 5e-4)}
+
+
+def _assert_lse(actual, expected, mode, label):
+    max_tol, mean_tol = LSE_TOL[mode]
+    finite = np.isfinite(expected)
+    assert np.array_equal(np.isfinite(actual), finite), f"{label}: -inf rows differ"
+    diff = np.abs(actual[finite] - expected[finite])
+    print(f"{label}: lse max_abs={diff.max():.3e} mean_abs={diff.mean():.3e}", flush=True)
+    assert diff.max() <= max_tol and diff.mean() <= mean_tol, f"{label}: lse outside {max_tol}/{mean_tol}"
+
+
+def _current_kv(cfg, seed):
+    """BF16 current K/V ``[Hkv, current_len, D]`` (unit normal) and the float64 copies."""
+    g = torch.Generator().manual_seed(seed)
+    shape = (cfg.num_kv_heads, cfg.current_len, cfg.head_dim)
+    k = torch.randn(shape, generator=g, dtype=torch.bfloat16)
+    v = torch.randn(shape, generator=g, dtype=torch.bfloat16)
+    return k, v, k.double().numpy(), v.double().numpy()
+
+
+def _history(problem, device, **kw):
+    gpu = problem.to(device)
+    kernel = make_history_attention_kernel(problem.config)
+    out, lse = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len,
+                      k_scale=problem.k_scale, v_scale=problem.v_scale, return_lse=True, **kw)
+    torch.cuda.synchronize()
+    return gpu, out, lse
+
+
+def _row_oracle(q, k, v, shape, rows, key_limit=None):
+    """float64 (out, lse) of selected (rank, q_head, token) rows over keys k/v [Hkv, L, D]."""
+    positions = orc.current_positions(shape)
+    outs, lses = [], []
+    for rank, qh, tok in rows.tolist():
+        kvh = orc.kv_head_for_query_head(qh, shape.num_q_heads, shape.num_kv_heads)
+        qrow = q[qh, positions[rank, tok]][None, None, :]
+        lim = None if key_limit is None else np.array([key_limit(positions[rank, tok])])
+        o, l = orc.attention_with_lse(qrow, k[kvh:kvh + 1], v[kvh:kvh + 1], shape.softmax_scale, lim)
+        outs.append(o[0, 0])
+        lses.append(l[0, 0])
+    return np.stack(outs), np.array(lses)
+
+
+@pytest.mark.parametrize(
+    "name,precision,exp2",
+    [
+        ("tiny-gqa4-d64-bf16", "auto", "fast"),
+        ("four-chip-fp8", "fp8", "fast"),
+        ("four-chip-fp8", "fp8", "exact"),
+        ("four-chip-fp8", "bf16", "fast"),
+        ("gqa8-d128-bf16", "auto", "fast"),
+    ],
+)
+def test_history_lse(name, precision, exp2, cuda_device):
+    problem = build_workload_problem(name, seed=21)
+    print(f"case {name} precision={precision} exp2={exp2}", flush=True)
+    kernel = make_history_attention_kernel(problem.config)
+    mode = "bf16" if kernel.uses_bf16_mfma(precision) else "fp8"
+    _, out, lse = _history(problem, cuda_device, precision=precision, exp2=exp2)
+    plain = kernel(*[t.to(cuda_device) for t in (problem.q_stacked, problem.kv_pages, problem.block_table)],
+                   page_valid_len=problem.page_valid_len.to(cuda_device), k_scale=problem.k_scale,
+                   v_scale=problem.v_scale, precision=precision, exp2=exp2)
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain), "writing the lse changed the output"
+    shape = orc.OracleShape.from_config(problem.config)
+    q, k, v = _real_history(problem)
+    length = problem.config.actual_history_len
+    rows = _sample_rows(shape, 128, seed=3)
+    eo, el = _row_oracle(q, k[:, :length], v[:, :length], shape, rows)
+    got = lse.cpu().numpy()[rows[:, 0], rows[:, 1], rows[:, 2]]
+    _assert_lse(got, el, mode, name)
+    _assert_close(out.float().cpu().numpy()[rows[:, 0], rows[:, 1], rows[:, 2]], eo, f"{name} output")
+
+
+@pytest.mark.parametrize("name", ["tiny-gqa4-d64-bf16", "four-chip-fp8", "gqa8-d128-bf16"])
+def test_current_causal_only(name, cuda_device):
+    """Causal attention among the current tokens, every row, with its lse."""
+    problem = build_workload_problem(name, seed=22)
+    cfg = problem.config
+    print(f"case {name}: current_len={cfg.current_len} il={cfg.interleave_size}", flush=True)
+    kc, vc, kc64, vc64 = _current_kv(cfg, seed=23)
+    kernel = CurrentAttentionKernel(cfg)
+    q = problem.q_stacked.to(cuda_device)
+    out, lse = kernel(q, stack_current_kv(kc, vc).to(cuda_device), return_lse=True)
+    torch.cuda.synchronize()
+    shape = orc.OracleShape.from_config(cfg)
+    q64 = problem.inputs.q.double().numpy()
+    eo, el = orc.expected_with_current(q64, kc64, vc64, shape)
+    _assert_close(out.float().cpu().numpy(), eo, f"{name} causal")
+    _assert_lse(lse.cpu().numpy(), el, "bf16", f"{name} causal")
+    # the first global token sees only itself: its output is its own V, exactly
+    pos = orc.current_positions(shape)
+    r0, t0 = np.argwhere(pos == 0)[0]
+    group = cfg.num_q_heads // cfg.num_kv_heads
+    first = out[r0, :, t0].cpu()
+    assert torch.equal(first, vc[:, 0].repeat_interleave(group, dim=0)), "token 0 output != its V"
+
+
+@pytest.mark.parametrize(
+    "name,precision,exp2",
+    [
+        ("tiny-gqa4-d64-bf16", "auto", "fast"),
+        ("four-chip-fp8", "fp8", "fast"),
+        ("four-chip-fp8", "fp8", "exact"),
+        ("four-chip-fp8", "bf16", "fast"),
+    ],
+)
+def test_prefill_merged_every_row(name, precision, exp2, cuda_device):
+    """History + causal current keys through PrefillAttention (in place), every row."""
+    problem = build_workload_problem(name, seed=24)
+    cfg = problem.config
+    print(f"case {name} precision={precision} exp2={exp2}", flush=True)
+    kc, vc, kc64, vc64 = _current_kv(cfg, seed=25)
+    gpu = problem.to(cuda_device)
+    kv_cur = stack_current_kv(kc, vc).to(cuda_device)
+    prefill = PrefillAttention(cfg)
+    out, lse = prefill(gpu.q_stacked, gpu.kv_pages, gpu.block_table, kv_cur, page_valid_len=gpu.page_valid_len,
+                       k_scale=problem.k_scale, v_scale=problem.v_scale, precision=precision, exp2=exp2,
+                       return_lse=True)
+    torch.cuda.synchronize()
+    shape = orc.OracleShape.from_config(cfg)
+    q, k, v = _real_history(problem)
+    eo, el = orc.expected_with_current(q, kc64, vc64, shape, k, v)
+    mode = "bf16" if prefill.history.uses_bf16_mfma(precision) else "fp8"
+    _assert_close(out.float().cpu().numpy(), eo, f"{name} merged")
+    _assert_lse(lse.cpu().numpy(), el, mode, f"{name} merged")
+    # a separate output buffer gives the same bits as the in-place merge
+    hist_out, hist_lse = prefill.history(gpu.q_stacked, gpu.kv_pages, gpu.block_table,
+                                         page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale,
+                                         v_scale=problem.v_scale, precision=precision, exp2=exp2,
+                                         return_lse=True)
+    separate = prefill.current(gpu.q_stacked, kv_cur, hist_out, hist_lse)
+    torch.cuda.synchronize()
+    assert torch.equal(separate, out)
+
+
+def test_prefill_full_config_sampled(cuda_device):
+    """The 64-rank configuration (131072 history + 4096 current tokens), sampled rows."""
+    problem = build_workload_problem("full-fp8", seed=26)
+    cfg = problem.config
+    print("case full-fp8 prefill", flush=True)
+    kc, vc, kc64, vc64 = _current_kv(cfg, seed=27)
+    gpu = problem.to(cuda_device)
+    out = PrefillAttention(cfg)(gpu.q_stacked, gpu.kv_pages, gpu.block_table, stack_current_kv(kc, vc).to(cuda_device),
+                                page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale,
+                                v_scale=problem.v_scale)
+    torch.cuda.synchronize()
+    shape = orc.OracleShape.from_config(cfg)
+    q, k, v = _real_history(problem)
+    length = cfg.actual_history_len
+    keys = np.concatenate([k[:, :length], kc64], axis=1)
+    vals = np.concatenate([v[:, :length], vc64], axis=1)
+    rows = _sample_rows(shape, 64, seed=28)
+    eo, _ = _row_oracle(q, keys, vals, shape, rows, key_limit=lambda g: length + g + 1)
+    _assert_close(out.float().cpu().numpy()[rows[:, 0], rows[:, 1], rows[:, 2]], eo, "full-fp8 merged sampled")
+
+
+@pytest.mark.parametrize("head_dim", [128, 256])
+def test_empty_history_merges_to_causal(head_dim, cuda_device):
+    """Pages with no valid token give lse -inf; merging them leaves the causal result unchanged."""
+    cfg = PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=4096, actual_history_len=4096,
+                             block_size=256, interleave_size=16, num_q_heads=8, head_dim=head_dim,
+                             backend="hip").validate()
+    problem = build_paged_problem(cfg, seed=29, kv_scale="per_tensor")
+    gpu = problem.to(cuda_device)
+    empty = torch.zeros_like(gpu.page_valid_len)
+    hist = make_history_attention_kernel(cfg)
+    h_out, h_lse = hist(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=empty, precision="fp8",
+                        return_lse=True)
+    kc, vc, _, _ = _current_kv(cfg, seed=30)
+    cur = CurrentAttentionKernel(cfg)
+    kv_cur = stack_current_kv(kc, vc).to(cuda_device)
+    merged = cur(gpu.q_stacked, kv_cur, h_out, h_lse)
+    alone = cur(gpu.q_stacked, kv_cur)
+    torch.cuda.synchronize()
+    assert torch.isneginf(h_lse).all() and not h_out.any()
+    assert torch.equal(merged, alone)

@@ -161,3 +161,94 @@ def test_expected_rows_agrees_with_stacked():
     full = orc.expected_stacked(q, k, v, shape)
     rows = np.array([[0, 0, 0], [1, 3, 63], [1, 1, 17]])
     np.testing.assert_allclose(orc.expected_rows(q, k, v, shape, rows), full[rows[:, 0], rows[:, 1], rows[:, 2]], atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# Log-sum-exp and current-token causal attention.
+# ---------------------------------------------------------------------------
+
+
+def test_lse_matches_fsum_loop_and_dense():
+    import math
+
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((4, 3, 6))
+    k = rng.standard_normal((2, 11, 6))
+    v = rng.standard_normal((2, 11, 6))
+    out, lse = orc.attention_with_lse(q, k, v, 0.41)
+    np.testing.assert_allclose(out, orc.dense_history_attention(q, k, v, 0.41), atol=1e-12)
+    for h in range(4):
+        for i in range(3):
+            scores = [float(q[h, i] @ k[h // 2, j]) * 0.41 for j in range(11)]
+            assert abs(lse[h, i] - math.log(math.fsum(math.exp(s) for s in scores))) < 1e-12
+
+
+def test_lse_closed_form_and_limits():
+    # n identical scores c -> lse = c + ln n; a row with no visible key -> -inf, zero output
+    q = np.ones((1, 3, 4))
+    k = np.full((1, 8, 4), 0.5)
+    v = np.random.default_rng(6).standard_normal((1, 8, 4))
+    out, lse = orc.attention_with_lse(q, k, v, 1.0, key_limit=np.array([8, 3, 0]))
+    np.testing.assert_allclose(lse[0, :2], [2.0 + np.log(8), 2.0 + np.log(3)], atol=1e-12)
+    np.testing.assert_allclose(out[0, 1], v[0, :3].mean(axis=0), atol=1e-12)
+    assert lse[0, 2] == -np.inf and not out[0, 2].any()
+
+
+def _sdpa(q, k, v, scale, mask=None, causal=False):
+    import torch.nn.functional as F
+
+    group = q.shape[0] // k.shape[0]
+    kk = torch.from_numpy(k).repeat_interleave(group, dim=0)
+    vv = torch.from_numpy(v).repeat_interleave(group, dim=0)
+    m = None if mask is None else torch.from_numpy(mask)
+    return F.scaled_dot_product_attention(torch.from_numpy(q), kk, vv, attn_mask=m, is_causal=causal, scale=scale).numpy()
+
+
+@pytest.mark.parametrize("pcp,il,q_len", [(1, 4, 16), (4, 1, 32), (2, 8, 64), (3, 2, 48)])
+def test_current_causal_matches_sdpa(pcp, il, q_len):
+    """Causal-only current attention, stacked by rank, equals torch's causal SDPA on the global order."""
+    cfg = PCPAttentionConfig(pcp_size=pcp, current_len=q_len, max_history_len=64 * pcp * il,
+                             actual_history_len=64 * pcp * il, interleave_size=il,
+                             block_size=64, head_dim=64, num_q_heads=4, backend="hip").validate()
+    shape = orc.OracleShape.from_config(cfg)
+    rng = np.random.default_rng(pcp * 100 + il)
+    q = rng.standard_normal((4, q_len, 64))
+    k = rng.standard_normal((2, q_len, 64))
+    v = rng.standard_normal((2, q_len, 64))
+    out, lse = orc.expected_with_current(q, k, v, shape)
+    ref = _sdpa(q, k, v, shape.softmax_scale, causal=True)
+    ref_stacked = np.stack(orc.shard_query(ref, shape))
+    np.testing.assert_allclose(out, ref_stacked, atol=1e-12)
+    # lse: the first global token sees only itself
+    pos = orc.current_positions(shape)
+    r0, t0 = np.argwhere(pos == 0)[0]
+    np.testing.assert_allclose(lse[r0, :, t0], (q[:, 0] * np.repeat(k[:, 0], 2, axis=0)).sum(-1) * shape.softmax_scale,
+                               atol=1e-12)
+
+
+def test_history_plus_current_matches_sdpa_and_merge():
+    """History keys (all visible) + causal current keys == SDPA with a boolean mask
+    over the concatenation; the log-sum-exp merge of the two parts gives the same."""
+    cfg = PCPAttentionConfig(pcp_size=2, current_len=32, max_history_len=256, actual_history_len=200,
+                             interleave_size=4, block_size=64, head_dim=64, num_q_heads=4, backend="hip").validate()
+    shape = orc.OracleShape.from_config(cfg)
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((4, 32, 64))
+    kh = rng.standard_normal((2, 256, 64))
+    vh = rng.standard_normal((2, 256, 64))
+    kc = rng.standard_normal((2, 32, 64))
+    vc = rng.standard_normal((2, 32, 64))
+    out, lse = orc.expected_with_current(q, kc, vc, shape, kh, vh)
+    mask = np.concatenate([np.ones((32, 200), bool), np.tril(np.ones((32, 32), bool))], axis=1)
+    ref = _sdpa(q, np.concatenate([kh[:, :200], kc], 1), np.concatenate([vh[:, :200], vc], 1), shape.softmax_scale,
+                mask=mask)
+    np.testing.assert_allclose(out, np.stack(orc.shard_query(ref, shape)), atol=1e-12)
+    # merge of the parts by log-sum-exp
+    hist = [orc.attention_with_lse(qs, kh[:, :200], vh[:, :200], shape.softmax_scale) for qs in orc.shard_query(q, shape)]
+    oh, lh = np.stack([h[0] for h in hist]), np.stack([h[1] for h in hist])
+    oc, lc = orc.expected_with_current(q, kc, vc, shape)
+    mx = np.maximum(lh, lc)
+    wh, wc = np.exp(lh - mx), np.exp(lc - mx)
+    merged = (wh[..., None] * oh + wc[..., None] * oc) / (wh + wc)[..., None]
+    np.testing.assert_allclose(merged, out, atol=1e-12)
+    np.testing.assert_allclose(mx + np.log(wh + wc), lse, atol=1e-12)
