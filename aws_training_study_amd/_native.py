@@ -37,6 +37,8 @@ DTYPE_FP8_E4M3FN = 2
 FLAG_BF16_MFMA = 1
 FLAG_EXACT_EXP2 = 2
 
+MAX_SPLITS = 64
+
 # Every symbol the header declares; the CPU test suite checks they resolve.
 EXPORTED_SYMBOLS = (
     "pcpa_abi_version",
@@ -44,6 +46,8 @@ EXPORTED_SYMBOLS = (
     "pcpa_check_params",
     "pcpa_history_attention",
     "pcpa_history_attention_lse",
+    "pcpa_history_attention_split",
+    "pcpa_split_workspace_bytes",
     "pcpa_current_attention",
     "pcpa_kv_cache_write",
     "pcpa_absmax_bf16",
@@ -119,6 +123,11 @@ def load_library() -> ctypes.CDLL:
     ]
     lib.pcpa_history_attention_lse.restype = ctypes.c_int32
     lib.pcpa_history_attention_lse.argtypes = [ctypes.POINTER(PcpaParams)] + [ctypes.c_void_p] * 7
+    lib.pcpa_split_workspace_bytes.restype = ctypes.c_int64
+    lib.pcpa_split_workspace_bytes.argtypes = [ctypes.POINTER(PcpaParams), ctypes.c_int32]
+    lib.pcpa_history_attention_split.restype = ctypes.c_int32
+    lib.pcpa_history_attention_split.argtypes = (
+        [ctypes.POINTER(PcpaParams), ctypes.c_int32] + [ctypes.c_void_p] * 7 + [ctypes.c_int64, ctypes.c_void_p])
     lib.pcpa_current_attention.restype = ctypes.c_int32
     lib.pcpa_current_attention.argtypes = [ctypes.POINTER(PcpaParams), ctypes.c_int32] + [ctypes.c_void_p] * 7
     lib.pcpa_kv_cache_write.restype = ctypes.c_int32

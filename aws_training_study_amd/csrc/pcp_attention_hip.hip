@@ -50,6 +50,7 @@ typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef short v4s __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
@@ -93,6 +94,12 @@ struct FwdArgs {
     const float* merge_lse;   // its per-row log-sum-exp
     int32_t interleave;       // striping of the current tokens over ranks
     int32_t pcp;
+    // Split history (overlap kernel, SPLIT): the table entries are cut into
+    // `splits` equal ranges, one per workgroup of a row tile; each writes its
+    // normalised FP32 partial output and log-sum-exp, merged afterwards.
+    int32_t splits;
+    float* part_o;            // [splits, pcp * Hq * local_q, D]
+    float* part_lse;          // [splits, pcp * Hq * local_q]
 };
 
 // ln(E[(1 + f) / 2^f]) for f uniform in [0, 1): how much the linear-mantissa
@@ -1241,19 +1248,31 @@ __device__ __forceinline__ void walk(const FwdArgs& a, uint8_t* lds, int wave, i
 
 // LSE: also write each row's log-sum-exp (a separate instantiation, so that
 // the plain one keeps its register allocation).
-template <int D, bool FAST, bool LSE>
+// SPLIT: the workgroup walks only its split's share of the table entries
+// and writes a normalised FP32 partial output and log-sum-exp (merged by
+// merge_splits_kernel).
+template <int D, bool FAST, bool LSE, bool SPLIT = false>
 __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     using S = Shape<D>;
     constexpr int QK = S::QK, DT = S::DT, ROW = S::ROW, CHUNKS = S::CHUNKS;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * S::RING];
 
     // ---- XCD-aware work mapping (as history_fwd_kernel) ---------------------
-    const int items = a.row_tiles * a.num_kv_heads;
+    // Items run row tile fastest, so an XCD's workgroups share one (KV head,
+    // split) and with it the pages they stream.
+    const int splits = SPLIT ? a.splits : 1;
+    const int items = a.row_tiles * a.num_kv_heads * splits;
     const int per_xcd = (items + 7) / 8;
     const int item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (item >= items) return;
-    const int head = item / a.row_tiles;
-    const int row_tile = item - head * a.row_tiles;
+    const int row_tile = item % a.row_tiles;
+    const int head = item / a.row_tiles / splits;
+    const int split = item / a.row_tiles - head * splits;
+    int entry_begin = 0;
+    if constexpr (SPLIT) {
+        entry_begin = (int)((int64_t)a.num_entries * split / splits);
+        a.num_entries = (int)((int64_t)a.num_entries * (split + 1) / splits);
+    }
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1343,7 +1362,7 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     v8i pbuf[2] = {v8i{}, v8i{}};
 
     // ---- pipeline --------------------------------------------------------------
-    const TileCursor first = next_tile(a, head, TileCursor{-1, 0, 0, 0});
+    const TileCursor first = next_tile(a, head, TileCursor{entry_begin - 1, 0, 0, 0});
     if (is_real(a, first)) {
         // V stages 2 and 3 stand for tiles -2 and -1: zeros.
         for (int idx = tid; idx < 2 * S::TILE / 16; idx += kThreads)
@@ -1367,12 +1386,27 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
 
     // ---- epilogue: O = O^T / l, bf16; log-sum-exp ---------------------------
     const float scale = sm.l > 0.f ? a.v_scale / sm.l : 0.f;
-    if (LSE && row_ok && h == 0) {
-        // sum_k exp(score_k) = l * 2^(m - 6), less the average overestimate
-        // of the linear-mantissa exp2
-        a.lse[row_off / (D * 2)] =
-            sm.l > 0.f ? __logf(sm.l) + (sm.m - kPBiasLog2) * kLn2 - (FAST ? kFastLseBias : 0.f) : -INFINITY;
+    // sum_k exp(score_k) = l * 2^(m - 6), less the average overestimate of
+    // the linear-mantissa exp2
+    const float lse =
+        sm.l > 0.f ? __logf(sm.l) + (sm.m - kPBiasLog2) * kLn2 - (FAST ? kFastLseBias : 0.f) : -INFINITY;
+    if constexpr (SPLIT) {
+        if (row_ok) {
+            const int64_t prow = (int64_t)split * a.rows_per_head * a.num_kv_heads + row_off / (D * 2);
+            float* const po = a.part_o + prow * D;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int d = 32 * dt + 8 * r4 + 4 * h;
+                    *(v4f*)(po + d) = v4f{o[dt][4 * r4 + 0] * scale, o[dt][4 * r4 + 1] * scale,
+                                          o[dt][4 * r4 + 2] * scale, o[dt][4 * r4 + 3] * scale};
+                }
+            if (h == 0) a.part_lse[prow] = lse;
+        }
+        return;
     }
+    if (LSE && row_ok && h == 0) a.lse[row_off / (D * 2)] = lse;
     if (row_ok) {
         uint8_t* const orow = a.out + row_off;
 #pragma unroll
@@ -1394,6 +1428,45 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
 }
 
 }  // namespace ovl
+
+// Merge of split partial outputs by log-sum-exp: one thread per (row, 8
+// consecutive d).  out = sum_s w_s O_s / sum_s w_s with w_s = e^(lse_s - max),
+// bf16; lse (optional) = max + ln(sum_s w_s).  HBM bound: 4 * D + 4 bytes read
+// per row and split, 2 * D written.
+__global__ void __launch_bounds__(256) merge_splits_kernel(const float* part_o, const float* part_lse, int splits,
+                                                           int64_t rows, int d_vec8, uint8_t* out, float* lse_out) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * d_vec8) return;
+    const int64_t row = idx / d_vec8;
+    const int d0 = (int)(idx - row * d_vec8) * 8;
+    const int D = d_vec8 * 8;
+    float mx = -INFINITY;
+    for (int sp = 0; sp < splits; ++sp) mx = fmaxf(mx, part_lse[sp * rows + row]);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float wsum = 0.f;
+    for (int sp = 0; sp < splits; ++sp) {
+        const float l = part_lse[sp * rows + row];
+        if (l == -INFINITY) continue;
+        const float w = __expf(l - mx);
+        wsum += w;
+        const float* const src = part_o + (sp * rows + row) * D + d0;
+        const v4f lo = *(const v4f*)src, hi = *(const v4f*)(src + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc[i] = fmaf(w, lo[i], acc[i]);
+            acc[4 + i] = fmaf(w, hi[i], acc[4 + i]);
+        }
+    }
+    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+    uint32_t wv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const __bf16 x0 = (__bf16)(acc[2 * i] * inv), x1 = (__bf16)(acc[2 * i + 1] * inv);
+        wv[i] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
+    }
+    *(v4i*)(out + (row * D + d0) * 2) = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
+    if (lse_out && d0 == 0) lse_out[row] = wsum > 0.f ? mx + __logf(wsum) : -INFINITY;
+}
 
 }  // namespace pcpa
 
@@ -1709,6 +1782,59 @@ int32_t pcpa_history_attention_lse(const pcpa_params* p, const void* q, const vo
     const hipError_t err =
         hipLaunchKernel(fn, dim3(8 * ((items + 7) / 8)), dim3(pcpa::kThreads), args, 0, (hipStream_t)stream);
     return err == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
+}
+
+int64_t pcpa_split_workspace_bytes(const pcpa_params* p, int32_t splits) {
+    const int32_t st = pcpa_check_params(p);
+    if (st != PCPA_OK) return st;
+    if (splits < 1 || splits > PCPA_MAX_SPLITS) return PCPA_ERR_BAD_SHAPE;
+    const int64_t rows = (int64_t)p->pcp_size * p->num_q_heads * p->local_q_len;
+    return (int64_t)splits * rows * ((int64_t)p->head_dim + 1) * 4;
+}
+
+int32_t pcpa_history_attention_split(const pcpa_params* p, int32_t splits, const void* q, const void* kv_pages,
+                                     const int32_t* block_table, const int32_t* page_valid_len, void* out,
+                                     float* lse, void* workspace, int64_t workspace_bytes, void* stream) {
+    const int64_t need = pcpa_split_workspace_bytes(p, splits);
+    if (need < 0) return (int32_t)need;
+    if (splits == 1) return pcpa_history_attention_lse(p, q, kv_pages, block_table, page_valid_len, out, lse, stream);
+    if (!q || !kv_pages || !block_table || !page_valid_len || !out || !workspace) return PCPA_ERR_NULL_POINTER;
+    if (((uintptr_t)q | (uintptr_t)kv_pages | (uintptr_t)out | (uintptr_t)workspace) & 15u) return PCPA_ERR_MISALIGNED;
+    if (((uintptr_t)block_table | (uintptr_t)page_valid_len | (uintptr_t)lse) & 3u) return PCPA_ERR_MISALIGNED;
+    if (workspace_bytes < need) return PCPA_ERR_BAD_SHAPE;
+    const bool fp8 = p->kv_dtype == PCPA_DTYPE_FP8_E4M3FN && !(p->flags & PCPA_FLAG_BF16_MFMA);
+    if (!fp8 || p->head_dim != 256) return PCPA_ERR_UNSUPPORTED;
+
+    pcpa::FwdArgs a = pcpa::common_args(p, q, out);
+    a.kv = (const uint8_t*)kv_pages;
+    a.block_table = block_table;
+    a.page_valid_len = page_valid_len;
+    a.head_stride = (int64_t)p->block_size * p->head_dim;
+    a.page_stride = 2 * (int64_t)p->num_kv_heads * a.head_stride;
+    a.num_entries = p->pcp_size * p->max_local_blocks;
+    a.num_pages = p->num_pages;
+    a.block_size = p->block_size;
+    a.score_scale = p->softmax_scale * p->k_scale * pcpa::kLog2e;
+    a.v_scale = p->v_scale;
+    a.row_tiles = (a.rows_per_head + pcpa::ovl::kRowsPerGroup - 1) / pcpa::ovl::kRowsPerGroup;
+    a.splits = splits;
+    const int64_t rows = (int64_t)p->pcp_size * p->num_q_heads * p->local_q_len;
+    a.part_o = (float*)workspace;
+    a.part_lse = a.part_o + (int64_t)splits * rows * p->head_dim;
+
+    void* args[] = {&a};
+    const void* fn = (p->flags & PCPA_FLAG_EXACT_EXP2) ? (const void*)pcpa::ovl::history_fwd_overlap<256, false, false, true>
+                                                       : (const void*)pcpa::ovl::history_fwd_overlap<256, true, false, true>;
+    const int items = a.row_tiles * p->num_kv_heads * splits;
+    hipError_t err = hipLaunchKernel(fn, dim3(8 * ((items + 7) / 8)), dim3(pcpa::ovl::kThreads), args, 0,
+                                     (hipStream_t)stream);
+    if (err != hipSuccess) return PCPA_ERR_LAUNCH;
+    const int d_vec8 = p->head_dim / 8;
+    const int64_t threads = rows * d_vec8;
+    hipLaunchKernelGGL(pcpa::merge_splits_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (const float*)a.part_o, (const float*)a.part_lse, splits, rows, d_vec8,
+                       (uint8_t*)out, lse);
+    return hipGetLastError() == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
 }
 
 int32_t pcpa_history_attention(const pcpa_params* p, const void* q, const void* kv_pages,

@@ -11,6 +11,7 @@ from .cache import KVCacheWriter, absmax, build_page_pool
 from .config import PCPAttentionConfig, get_preset
 from .current import CurrentAttentionKernel, PrefillAttention, stack_current_kv
 from .kernel import make_history_attention_kernel, pack_local_kv, wrap_for_native_torch
+from .launch import GraphedLaunch
 from .layout import (
     gather_history,
     global_positions_for_rank,
@@ -24,6 +25,7 @@ from .paging import make_block_table, pack_page_pool, page_valid_lengths, valid_
 
 __all__ = [
     "CurrentAttentionKernel",
+    "GraphedLaunch",
     "KVCacheWriter",
     "PCPAttentionConfig",
     "absmax",

@@ -140,6 +140,12 @@ class PrefillAttention:
         self.current = CurrentAttentionKernel(config)
         self.config = self.history.config
 
+    def graphed(self, q, kv_pages, block_table, kv_current, *, warmup: int = 1, **kwargs):
+        """Both launches captured into one HIP graph (``launch.GraphedLaunch``)."""
+        from .launch import GraphedLaunch
+
+        return GraphedLaunch(lambda: self(q, kv_pages, block_table, kv_current, **kwargs), warmup=warmup)
+
     def __call__(self, q, kv_pages, block_table, kv_current, block_valid_mask=None, *, page_valid_len=None,
                  k_scale: float = 1.0, v_scale: float = 1.0, precision: str = "auto", exp2: str = "fast",
                  return_lse: bool = False):

@@ -86,6 +86,10 @@ class HistoryAttentionKernel:
       normalisation); ``"exact"`` rounds ``v_exp_f32``.  Other paths always
       use ``v_exp_f32``.
 
+    * ``splits``: for the e4m3 head_dim-256 kernel, cut the history into this
+      many ranges run by separate workgroups and merged by log-sum-exp (a
+      device workspace is allocated and kept); ``"auto"`` splits only when
+      the (row tile, KV head) workgroups would leave CUs idle.
     * ``return_lse``: also return each row's log-sum-exp (float32
       ``[pcp, Hq, local_q]``, natural log of the sum of ``exp(score)`` over
       the valid history keys, ``-inf`` for none) - the input of a merge with
@@ -156,6 +160,7 @@ class HistoryAttentionKernel:
         precision: str = "auto",
         exp2: str = "fast",
         return_lse: bool = False,
+        splits="auto",
     ):
         import torch
 
@@ -207,24 +212,103 @@ class HistoryAttentionKernel:
         if return_lse:
             lse = torch.empty(q_shape[:3], dtype=torch.float32, device=device)
         params = self._params(num_pages, k_scale, v_scale)
-        if self.uses_bf16_mfma(precision):
+        bf16_mfma = self.uses_bf16_mfma(precision)
+        if bf16_mfma:
             params.flags |= self._native.FLAG_BF16_MFMA
         if exp2 == "exact":
             params.flags |= self._native.FLAG_EXACT_EXP2
+        n_split = self.split_count(device, bf16_mfma) if splits == "auto" else int(splits)
         with torch.cuda.device(device):
             stream = torch.cuda.current_stream(device).cuda_stream
-            status = self._lib.pcpa_history_attention_lse(
-                ctypes.byref(params),
-                q.data_ptr(),
-                kv_pages.data_ptr(),
-                block_table.data_ptr(),
-                page_valid_len.data_ptr(),
-                out.data_ptr(),
-                None if lse is None else lse.data_ptr(),
-                stream,
-            )
+            if n_split > 1:
+                workspace = self._workspace(params, n_split, device)
+                status = self._lib.pcpa_history_attention_split(
+                    ctypes.byref(params),
+                    n_split,
+                    q.data_ptr(),
+                    kv_pages.data_ptr(),
+                    block_table.data_ptr(),
+                    page_valid_len.data_ptr(),
+                    out.data_ptr(),
+                    None if lse is None else lse.data_ptr(),
+                    workspace.data_ptr(),
+                    workspace.numel(),
+                    stream,
+                )
+            else:
+                status = self._lib.pcpa_history_attention_lse(
+                    ctypes.byref(params),
+                    q.data_ptr(),
+                    kv_pages.data_ptr(),
+                    block_table.data_ptr(),
+                    page_valid_len.data_ptr(),
+                    out.data_ptr(),
+                    None if lse is None else lse.data_ptr(),
+                    stream,
+                )
         self._native.check(status)
         return (out, lse) if return_lse else out
+
+    def graphed(self, q, kv_pages, block_table, block_valid_mask=None, *, warmup: int = 1, **kwargs):
+        """This call captured into a HIP graph (``launch.GraphedLaunch``).
+
+        The output buffer (``out=``, allocated here if not given) and the
+        log-sum-exp (``return_lse=True``) are fixed; ``replay()`` recomputes
+        them from the current contents of the same input tensors.
+        """
+        import torch
+
+        from .launch import GraphedLaunch
+
+        if kwargs.get("out") is None:
+            kwargs["out"] = torch.empty_like(q)
+        page_valid_len = kwargs.pop("page_valid_len", None)
+        if page_valid_len is None:
+            if block_valid_mask is not None:
+                from .paging import valid_lengths_from_block_mask
+
+                page_valid_len = valid_lengths_from_block_mask(block_valid_mask, self.config)
+            else:
+                page_valid_len = self.default_page_valid_len(q.device)
+        page_valid_len = page_valid_len.to(device=q.device, dtype=torch.int32).contiguous()
+        block_table = block_table.to(device=q.device, dtype=torch.int32).contiguous()
+        return GraphedLaunch(
+            lambda: self(q, kv_pages, block_table, page_valid_len=page_valid_len, **kwargs), warmup=warmup)
+
+    # Each workgroup of the e4m3 head_dim-256 kernel takes 256 query rows of
+    # one KV head and a whole CU.
+    ROWS_PER_WORKGROUP = 256
+    # A split should still walk at least this many 64-key tiles.
+    MIN_TILES_PER_SPLIT = 16
+
+    def split_count(self, device, bf16_mfma: bool) -> int:
+        """History splits for ``splits="auto"``: enough (row tile, KV head,
+        split) workgroups to give every CU one, for the e4m3 head_dim-256
+        kernel; 1 elsewhere or when the row tiles already fill the GPU."""
+        import torch
+
+        cfg = self.config
+        if bf16_mfma or cfg.kv_dtype != "fp8_e4m3fn" or cfg.head_dim != 256:
+            return 1
+        rows_per_head = cfg.pcp_size * cfg.local_q_len * (cfg.num_q_heads // cfg.num_kv_heads)
+        items = -(-rows_per_head // self.ROWS_PER_WORKGROUP) * cfg.num_kv_heads
+        cus = torch.cuda.get_device_properties(device).multi_processor_count
+        if items >= cus:
+            return 1
+        tiles = -(-cfg.actual_history_len // 64)
+        return max(1, min(self._native.MAX_SPLITS, -(-cus // items), tiles // self.MIN_TILES_PER_SPLIT))
+
+    def _workspace(self, params, n_split: int, device):
+        import torch
+
+        size = self._lib.pcpa_split_workspace_bytes(ctypes.byref(params), n_split)
+        if size < 0:
+            self._native.check(int(size))
+        ws = getattr(self, "_split_ws", None)
+        if ws is None or ws.device != device or ws.numel() < size:
+            ws = torch.empty(size, dtype=torch.uint8, device=device)
+            self._split_ws = ws
+        return ws
 
 
 def make_history_attention_kernel(config: PCPAttentionConfig) -> HistoryAttentionKernel:

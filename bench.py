@@ -45,10 +45,11 @@ def parse_args(argv=None):
     parser.add_argument("--steps", type=int, default=30)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--workload", default="full-fp8")
-    parser.add_argument("--path", choices=("history", "cache-write", "current"), default="history",
+    parser.add_argument("--path", choices=("history", "cache-write", "current", "launch"), default="history",
                         help="history: the attention launch (the headline metric); cache-write: the KV-cache "
                              "producer filling the workload's page pool from BF16 K/V; current: causal attention "
-                             "of the current tokens merged with the history output")
+                             "of the current tokens merged with the history output; launch: per-call latency of "
+                             "the workload's history attention, eager calls against a replayed HIP graph")
     parser.add_argument("--seed", type=int, default=1234)
     parser.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
                         help="approximate CPU time budget of the ring-model baseline sample")
@@ -340,6 +341,72 @@ def current_bench(args) -> int:
     return 0
 
 
+def launch_bench(args) -> int:
+    """Per-call host-inclusive latency (call + synchronise) and back-to-back call rate, eager vs HIP graph."""
+    import torch
+
+    from aws_training_study_amd.pcp_attention import make_history_attention_kernel
+    from aws_training_study_amd.pcp_attention.workloads import build_workload_problem, get_workload
+
+    workload = get_workload(args.workload)
+    problem = build_workload_problem(workload, args.seed)
+    cfg = problem.config
+    device = torch.device("cuda", 0)
+    gpu = problem.to(device)
+    kernel = make_history_attention_kernel(cfg)
+    out = torch.empty_like(gpu.q_stacked)
+    kw = dict(page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale, v_scale=problem.v_scale, out=out)
+
+    def eager():
+        kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, **kw)
+
+    graphed = kernel.graphed(gpu.q_stacked, gpu.kv_pages, gpu.block_table, **kw)
+    calls = max(args.steps, 50)
+
+    def measure(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        lat = []
+        for _ in range(calls):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            lat.append((time.perf_counter() - t0) * 1e3)
+        lat.sort()
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        torch.cuda.synchronize()
+        rate_ms = (time.perf_counter() - t0) * 1e3 / calls
+        return {"median_ms": round(statistics.median(lat), 4), "mean_ms": round(statistics.fmean(lat), 4),
+                "p90_ms": round(lat[max(0, (9 * calls + 9) // 10 - 1)], 4), "back_to_back_ms": round(rate_ms, 4)}
+
+    e, g = measure(eager), measure(graphed.replay)
+    result = {
+        "metric": "per-call latency ms (call + synchronise), history attention, eager vs HIP graph, 1 GPU",
+        "value": g["median_ms"],
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": calls,
+        "warmup": args.warmup,
+        "ms_per_step": g["median_ms"],
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3" if cfg.kv_dtype == "fp8_e4m3fn" else "bf16",
+        "data": "synthetic (seeded, as the history bench)",
+        "config": {"workload": workload.name, "pcp_ranks": cfg.pcp_size, "current_tokens": cfg.current_len,
+                   "history_tokens": cfg.actual_history_len, "q_heads": cfg.num_q_heads,
+                   "kv_heads": cfg.num_kv_heads, "head_dim": cfg.head_dim,
+                   "splits": kernel.split_count(device, kernel.uses_bf16_mfma())},
+        "eager": e,
+        "graph": g,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
@@ -358,6 +425,8 @@ def main(argv=None) -> int:
         return cache_write_bench(args)
     if args.path == "current":
         return current_bench(args)
+    if args.path == "launch":
+        return launch_bench(args)
 
     import torch
 

@@ -137,6 +137,28 @@ int32_t pcpa_history_attention_lse(const pcpa_params* params, const void* q, con
                                    void* out, float* lse, void* stream);
 
 /*
+ * Split history for workloads with few query rows: the table entries are cut
+ * into `splits` equal ranges, each (row tile, range) pair runs as its own
+ * workgroup and writes a normalised FP32 partial output and log-sum-exp into
+ * `workspace`, and a second launch merges the partials by log-sum-exp into
+ * `out` (and `lse`, optional).  Results equal pcpa_history_attention_lse's to
+ * rounding.  For a launch whose (row tile, KV head) workgroups would leave
+ * CUs idle (one workgroup of 256 rows per CU).  e4m3 MFMA path at head_dim
+ * 256 only (else PCPA_ERR_UNSUPPORTED); splits in [1, PCPA_MAX_SPLITS]
+ * (1 = pcpa_history_attention_lse).  workspace: device memory of at least
+ * pcpa_split_workspace_bytes(params, splits) bytes, 16-byte aligned; its
+ * contents need no initialisation and are left undefined.  The library does
+ * not allocate it.  No reference counterpart (the reference's device ring
+ * has no split).
+ */
+#define PCPA_MAX_SPLITS 64
+int64_t pcpa_split_workspace_bytes(const pcpa_params* params, int32_t splits);
+int32_t pcpa_history_attention_split(const pcpa_params* params, int32_t splits, const void* q,
+                                     const void* kv_pages, const int32_t* block_table,
+                                     const int32_t* page_valid_len, void* out, float* lse,
+                                     void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Causal attention of the current tokens among themselves, optionally merged
  * with a history result: the step after the history attention.  The
  * reference stops at history-only attention ("current tokens do not attend

@@ -25,7 +25,7 @@ def lib():
 
 def _declared_functions():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int32_t|const char\*)\s+(pcpa_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int32_t|int64_t|const char\*)\s+(pcpa_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_what_python_binds():
@@ -151,3 +151,22 @@ def test_lse_and_current_entries_validate_without_a_gpu(lib):
     assert c(ctypes.byref(p), 16, 8, 16, None, None, 16, None, None) == -6      # q alignment
     assert c(ctypes.byref(p), 16, 16, 16, 16, 2, 16, None, None) == -6          # hist_lse alignment
     assert c(ctypes.byref(p), 16, 16, 16, None, None, 16, 2, None) == -6        # lse alignment
+
+
+def test_split_entry_validates_without_a_gpu(lib):
+    """pcpa_split_workspace_bytes / pcpa_history_attention_split errors come back before any HIP call."""
+    p = _good_params(kv_dtype=2, head_dim=256)  # 4 ranks x 8 heads x 64 tokens = 2048 rows
+    size = lib.pcpa_split_workspace_bytes(ctypes.byref(p), 3)
+    assert size == 3 * 2048 * (256 + 1) * 4
+    assert lib.pcpa_split_workspace_bytes(ctypes.byref(p), 0) == -3
+    assert lib.pcpa_split_workspace_bytes(ctypes.byref(p), 65) == -3
+    assert lib.pcpa_split_workspace_bytes(ctypes.byref(_good_params(abi_version=2)), 2) == -2
+    size = lib.pcpa_split_workspace_bytes(ctypes.byref(p), 2)
+    f = lib.pcpa_history_attention_split
+    assert f(ctypes.byref(p), 2, 16, 16, 16, 16, 16, None, None, size, None) == -1          # workspace
+    assert f(ctypes.byref(p), 2, 16, 16, 16, 16, 16, None, 16, size - 16, None) == -3       # too small
+    assert f(ctypes.byref(p), 2, 16, 16, 16, 16, 16, None, 8, size, None) == -6             # alignment
+    assert f(ctypes.byref(p), 2, 16, 16, 16, 16, 16, 2, 16, size, None) == -6               # lse alignment
+    assert f(ctypes.byref(_good_params(head_dim=256)), 2, 16, 16, 16, 16, 16, None, 16, size, None) == -5  # bf16
+    assert f(ctypes.byref(_good_params(kv_dtype=2, head_dim=256, flags=1)), 2, 16, 16, 16, 16, 16, None, 16, size,
+             None) == -5                                                                    # BF16 MFMAs

@@ -1,0 +1,98 @@
+"""GPU parity of the split-history path (pcpa_history_attention_split): the
+history is cut into ranges run by separate workgroups and merged by
+log-sum-exp.  Bar as for the one-pass kernel (max-abs <= 2e-2, mean-abs <=
+2e-3 against float64); the merged log-sum-exp within the e4m3 bound of
+tests/test_gpu_current.py; against the one-pass result within rounding.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from aws_training_study_amd.pcp_attention import make_history_attention_kernel
+from aws_training_study_amd.pcp_attention.config import PCPAttentionConfig
+from aws_training_study_amd.pcp_attention.workloads import build_paged_problem, build_workload_problem
+from oracle import pcp_oracle as orc
+
+from test_gpu_current import _assert_lse
+from test_gpu_parity import _assert_close, _real_history
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(problem, device, **kw):
+    gpu = problem.to(device)
+    kernel = make_history_attention_kernel(problem.config)
+    res = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len,
+                 k_scale=problem.k_scale, v_scale=problem.v_scale, precision="fp8", **kw)
+    torch.cuda.synchronize()
+    return res
+
+
+@pytest.mark.parametrize("splits", [2, 3, 4, 8])
+def test_split_matches_oracle_and_one_pass(splits, cuda_device):
+    problem = build_workload_problem("four-chip-fp8", seed=31)
+    print(f"case four-chip-fp8 splits={splits}", flush=True)
+    out, lse = _run(problem, cuda_device, splits=splits, return_lse=True)
+    one, one_lse = _run(problem, cuda_device, splits=1, return_lse=True)
+    shape = orc.OracleShape.from_config(problem.config)
+    q, k, v = _real_history(problem)
+    length = problem.config.actual_history_len
+    exp = orc.expected_stacked(q, k, v, shape)
+    _assert_close(out.float().cpu().numpy(), exp, f"split {splits}")
+    diff = (out.float() - one.float()).abs()
+    print(f"split {splits} vs one pass: max {diff.max().item():.3e} mean {diff.mean().item():.3e}", flush=True)
+    # each range takes its own running max, so P is rounded to e4m3 against
+    # another reference: the two differ by e4m3 noise, not by a bias
+    assert diff.max().item() <= 1e-2 and diff.mean().item() <= 1e-3
+    lse_diff = (lse - one_lse).abs()
+    print(f"split {splits} lse vs one pass: max {lse_diff.max().item():.3e} mean {lse_diff.mean().item():.3e}",
+          flush=True)
+    assert lse_diff.max().item() <= 1e-2 and lse_diff.mean().item() <= 2e-3
+    rows = np.array([[0, 0, 0], [15, 31, 63], [7, 12, 20]])
+    _, el = [], []
+    for rank, qh, tok in rows.tolist():
+        pos = orc.current_positions(shape)[rank, tok]
+        kvh = orc.kv_head_for_query_head(qh, shape.num_q_heads, shape.num_kv_heads)
+        _, l = orc.attention_with_lse(q[qh, pos][None, None], k[kvh:kvh + 1, :length], v[kvh:kvh + 1, :length],
+                                      shape.softmax_scale)
+        el.append(l[0, 0])
+    _assert_lse(lse.cpu().numpy()[rows[:, 0], rows[:, 1], rows[:, 2]], np.array(el), "fp8", f"split {splits}")
+
+
+def test_auto_splits_small_workload(cuda_device):
+    """The 16-rank workload leaves CUs idle with one workgroup per (row tile, KV head): auto splits it."""
+    problem = build_workload_problem("four-chip-fp8", seed=32)
+    kernel = make_history_attention_kernel(problem.config)
+    n = kernel.split_count(cuda_device, bf16_mfma=False)
+    print(f"auto splits on {torch.cuda.get_device_properties(cuda_device).multi_processor_count} CUs: {n}", flush=True)
+    assert n > 1
+    full = build_workload_problem("full-fp8", seed=1234)
+    assert make_history_attention_kernel(full.config).split_count(cuda_device, bf16_mfma=False) == 1
+    out = _run(problem, cuda_device)
+    q, k, v = _real_history(problem)
+    _assert_close(out.float().cpu().numpy(), orc.expected_stacked(q, k, v, orc.OracleShape.from_config(problem.config)),
+                  "auto split")
+
+
+@pytest.mark.parametrize("actual,splits", [(1, 4), (1000, 3), (4096 - 1, 64), (2048, 7)])
+def test_split_unaligned_and_empty_ranges(actual, splits, cuda_device):
+    """Partial pages, and splits whose entry range holds no valid token (lse -inf, merged away)."""
+    cfg = PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=4096, actual_history_len=actual,
+                             block_size=256, interleave_size=64, backend="hip").validate()
+    problem = build_paged_problem(cfg, seed=actual + splits, kv_scale="per_tensor")
+    print(f"case actual={actual} splits={splits} entries={cfg.pcp_size * cfg.max_local_blocks}", flush=True)
+    out = _run(problem, cuda_device, splits=splits).float().cpu().numpy()
+    one = _run(problem, cuda_device, splits=1).float().cpu().numpy()
+    q, k, v = _real_history(problem)
+    shape = orc.OracleShape.from_config(cfg)
+    exp = orc.expected_stacked(q, k, v, shape)
+    assert np.isfinite(out).all()
+    # the e4m3 rounding of Q and P dominates at short histories; compare with the one-pass kernel as well
+    max_abs, mean_abs = orc.max_abs_and_mean_abs(out, exp)
+    one_max, _ = orc.max_abs_and_mean_abs(one, exp)
+    print(f"split max_abs={max_abs:.3e} mean_abs={mean_abs:.3e} (one pass max_abs={one_max:.3e})", flush=True)
+    assert max_abs <= max(2e-2, one_max + 4e-3) and mean_abs <= 2e-3
+    assert np.abs(out - one).max() <= 1e-2
