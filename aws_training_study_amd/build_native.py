@@ -1,8 +1,9 @@
 """Build the gfx950 HIP library in-tree with hipcc.
 
 ``python -m aws_training_study_amd.build_native`` compiles
-``csrc/pcp_attention_hip.hip`` into ``_lib/libpcp_attention_hip.so``.  hipcc
-cross-compiles for gfx950 without a GPU present.
+``csrc/pcp_attention_hip.hip`` (which includes the kernel headers in
+``csrc/``) into ``_lib/libpcp_attention_hip.so``.  hipcc cross-compiles for
+gfx950 without a GPU present.
 """
 
 from __future__ import annotations

@@ -1,0 +1,191 @@
+// KV-cache producer kernels (quantise + page write, absolute maximum).
+#pragma once
+
+#include "common.hpp"
+
+// ============================================================================
+// KV-cache producer: per-tensor e4m3 quantisation of K/V and the page write
+// in pack_local_kv's format (kernel.py:17-29), i.e. what the reference does
+// on the host with shard_history (layout.py:54-98), the float8 cast
+// (run_poc.py:96-103) and pack_local_kv, done on the GPU for a range of
+// global history positions (a whole history, or tokens appended to it).
+// Both kernels are HBM bound: 2 bytes read and 1 (e4m3) or 2 (bf16) bytes
+// written per element.
+// ============================================================================
+namespace pcpa {
+namespace cache {
+
+constexpr int kThreads = 256;
+
+// floor(n / d) for 0 <= n < 2^31 by one 64-bit multiply: M = ceil(2^(32+s)/d)
+// with 2^s >= d gives the exact quotient for every n < 2^32.
+struct FastDiv {
+    uint64_t m;
+    uint32_t shift;
+    uint32_t d;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t s = 0;
+    while ((1ull << s) < d) ++s;
+    const unsigned __int128 num = (unsigned __int128)1 << (32 + s);
+    return FastDiv{(uint64_t)((num + d - 1) / d), 32 + s, d};
+}
+__device__ __forceinline__ uint32_t div(uint32_t n, const FastDiv& f) {
+    return (uint32_t)(((unsigned __int128)n * f.m) >> f.shift);
+}
+
+struct WriteArgs {
+    const uint8_t* k;   // [Hkv, n, D] bf16
+    const uint8_t* v;
+    const int32_t* block_table;
+    int32_t* page_valid_len;  // optional
+    uint8_t* pages;
+    int64_t page_stride;      // bytes of one page
+    int64_t head_stride;      // bytes of one head's K (or V) block in a page
+    int64_t v_offset;         // bytes from a page's K to its V
+    FastDiv chunks_per_row;   // D / 8
+    FastDiv interleave;
+    FastDiv pcp;
+    FastDiv block;            // block_size
+    uint32_t log2_cpr, log2_il, log2_pcp, log2_block;  // when POW2
+    uint32_t num_tokens;
+    uint32_t first_pos;
+    int32_t max_local_blocks;
+    int32_t num_pages;
+    int32_t head_dim;
+    float k_scale, v_scale;
+};
+
+// e4m3 code of x (round to nearest even; magnitudes above 464 and infinities
+// become the NaN code 0x7f with x's sign, like torch's float8_e4m3fn cast;
+// v_cvt_pk_fp8_f32 agrees except that it writes 0xff for every NaN input).
+__device__ __forceinline__ uint32_t e4m3_codes4(float a, float b, float c, float d) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    uint32_t u = (uint32_t)w;
+    const float x[4] = {a, b, c, d};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (__builtin_isnan(x[i])) {
+            const uint32_t code = (__float_as_uint(x[i]) >> 31) ? 0xffu : 0x7fu;
+            u = (u & ~(0xffu << (8 * i))) | (code << (8 * i));
+        }
+    return u;
+}
+
+// One thread per (token, 8-element chunk) of head blockIdx.y: the token's
+// page row comes from the striped layout (owner rank, local position) and
+// the block table.  POW2: pcp, interleave, block size and D / 8 are powers
+// of two (every configuration in use), so the maps are shifts and masks.
+// Tokens whose table entry is outside [0, num_pages) are skipped, as the
+// attention kernel skips such pages.
+template <bool FP8, bool POW2>
+__global__ void __launch_bounds__(kThreads) kv_write_kernel(WriteArgs a, uint32_t row_chunks) {
+    const uint32_t gid = blockIdx.x * kThreads + threadIdx.x;
+    if (gid >= row_chunks) return;
+    const uint32_t head = blockIdx.y;
+    uint32_t token, chunk, owner, local, blk, slot;
+    const uint32_t p0 = a.first_pos;
+    if constexpr (POW2) {
+        token = gid >> a.log2_cpr;
+        chunk = gid & ((1u << a.log2_cpr) - 1);
+        const uint32_t p = p0 + token;
+        const uint32_t c = p >> a.log2_il;
+        owner = c & ((1u << a.log2_pcp) - 1);
+        local = ((c >> a.log2_pcp) << a.log2_il) | (p & ((1u << a.log2_il) - 1));
+        blk = local >> a.log2_block;
+        slot = local & ((1u << a.log2_block) - 1);
+    } else {
+        token = div(gid, a.chunks_per_row);
+        chunk = gid - token * a.chunks_per_row.d;
+        const uint32_t p = p0 + token;
+        const uint32_t c = div(p, a.interleave);
+        const uint32_t rounds = div(c, a.pcp);
+        owner = c - rounds * a.pcp.d;
+        local = rounds * a.interleave.d + (p - c * a.interleave.d);
+        blk = div(local, a.block);
+        slot = local - blk * a.block.d;
+    }
+    const uint32_t row = head * a.num_tokens + token;
+    if (blk >= (uint32_t)a.max_local_blocks) return;  // excluded by the host's capacity check
+    const int32_t entry = (int32_t)(owner * a.max_local_blocks + blk);
+    const int32_t page = a.block_table[entry];
+    if ((uint32_t)page >= (uint32_t)a.num_pages) return;
+    if (a.page_valid_len && head == 0 && chunk == 0) atomicMax(a.page_valid_len + entry, (int32_t)slot + 1);
+
+    const int64_t src = ((int64_t)row * a.head_dim + chunk * 8) * 2;  // [Hkv, n, D] bf16
+    const v4i kin = *(const v4i*)(a.k + src);
+    const v4i vin = *(const v4i*)(a.v + src);
+    const int64_t es = FP8 ? 1 : 2;
+    uint8_t* const dst = a.pages + (int64_t)page * a.page_stride + head * a.head_stride +
+                         ((int64_t)slot * a.head_dim + chunk * 8) * es;
+    if constexpr (FP8) {
+        float kf[8], vf[8];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            // x / scale with IEEE division, as torch computes (x / scale).to(float8)
+            kf[2 * w] = bf16_bits_to_f32((uint32_t)kin[w] & 0xffffu) / a.k_scale;
+            kf[2 * w + 1] = bf16_bits_to_f32((uint32_t)kin[w] >> 16) / a.k_scale;
+            vf[2 * w] = bf16_bits_to_f32((uint32_t)vin[w] & 0xffffu) / a.v_scale;
+            vf[2 * w + 1] = bf16_bits_to_f32((uint32_t)vin[w] >> 16) / a.v_scale;
+        }
+        *(v2i*)dst = v2i{(int)e4m3_codes4(kf[0], kf[1], kf[2], kf[3]), (int)e4m3_codes4(kf[4], kf[5], kf[6], kf[7])};
+        *(v2i*)(dst + a.v_offset) =
+            v2i{(int)e4m3_codes4(vf[0], vf[1], vf[2], vf[3]), (int)e4m3_codes4(vf[4], vf[5], vf[6], vf[7])};
+    } else {
+        *(v4i*)dst = kin;
+        *(v4i*)(dst + a.v_offset) = vin;
+    }
+}
+
+// max |x| over n bf16 values into *out (as the bits of a non-negative float,
+// ordered like unsigned integers); *out is cleared first by init_kernel.
+__global__ void absmax_init_kernel(uint32_t* out) { *out = 0u; }
+
+// Workgroup b reduces the contiguous span [b * span, (b + 1) * span) with
+// four 16-byte loads in flight per thread, then one atomic per workgroup.
+__global__ void __launch_bounds__(kThreads) absmax_kernel(const uint16_t* x, int64_t n, int64_t span,
+                                                          uint32_t* out) {
+    constexpr int kVec = 8, kUnroll = 4, kStep = kThreads * kVec;
+    __shared__ float partial[kThreads / 64];
+    const int64_t begin = (int64_t)blockIdx.x * span;
+    const int64_t end = begin + span < n ? begin + span : n;
+    float m[kUnroll] = {0.f, 0.f, 0.f, 0.f};
+    int64_t i = begin + threadIdx.x * kVec;
+    for (; i + (kUnroll - 1) * kStep + kVec <= end; i += kUnroll * kStep) {
+        v4i raw[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) raw[u] = *(const v4i*)(x + i + u * kStep);
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                m[u] = fmaxf(m[u], fabsf(bf16_bits_to_f32((uint32_t)raw[u][w] & 0xffffu)));
+                m[u] = fmaxf(m[u], fabsf(bf16_bits_to_f32((uint32_t)raw[u][w] >> 16)));
+            }
+    }
+    for (; i < end; i += kStep) {
+        if (i + kVec <= end) {
+            const v4i raw = *(const v4i*)(x + i);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                m[0] = fmaxf(m[0], fabsf(bf16_bits_to_f32((uint32_t)raw[w] & 0xffffu)));
+                m[0] = fmaxf(m[0], fabsf(bf16_bits_to_f32((uint32_t)raw[w] >> 16)));
+            }
+        } else {
+            for (int64_t e = i; e < end; ++e) m[0] = fmaxf(m[0], fabsf(bf16_bits_to_f32(x[e])));
+        }
+    }
+    float r = fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) r = fmaxf(r, __shfl_xor(r, off));
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = r;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kThreads / 64; ++w) r = fmaxf(r, partial[w]);
+        atomicMax(out, __float_as_uint(r));
+    }
+}
+
+}  // namespace cache
+}  // namespace pcpa

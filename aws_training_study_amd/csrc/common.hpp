@@ -1,0 +1,230 @@
+// Shared types, constants, launch arguments, LDS layout maps and the
+// block-table walk of the history attention kernels (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "pcp_attention_hip.h"
+
+namespace pcpa {
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+#define PCPA_LDS(T, p) ((__attribute__((address_space(3))) T*)(p))
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRowsPerWave = 32;
+constexpr int kRowsPerGroup = kWaves * kRowsPerWave;
+constexpr int kKeyTile = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kFp8Max = 448.0f;
+// FP8 probabilities are computed as 2^(x - m + kPBiasLog2): the largest is 64,
+// and values down to 2^-12 of the row max stay in e4m3's normal range.  The
+// factor cancels in O / l because l sums the same biased values.
+constexpr float kPBiasLog2 = 6.0f;
+
+struct FwdArgs {
+    const uint8_t* q;
+    const uint8_t* kv;
+    const int32_t* block_table;
+    const int32_t* page_valid_len;
+    uint8_t* out;
+    int64_t page_stride;   // bytes of one page (K and V of every KV head)
+    int64_t head_stride;   // bytes of one head's K (or V) block
+    int32_t rows_per_head; // pcp * group * local_q
+    int32_t row_tiles;     // ceil(rows_per_head / kRowsPerGroup)
+    int32_t group_rows;    // group * local_q
+    int32_t local_q;
+    int32_t num_q_heads;
+    int32_t group;
+    int32_t num_kv_heads;
+    int32_t num_entries;   // pcp * max_local_blocks
+    int32_t num_pages;
+    int32_t block_size;
+    float score_scale;     // softmax_scale * k_scale * log2(e)
+    float v_scale;
+    float* lse;            // optional: natural-log sum of exp(score) per row, [pcp, Hq, local_q]
+    // Causal current-token attention only (history_fwd_kernel<..., CAUSAL>):
+    const uint8_t* merge_o;   // optional history output to merge with, bf16 like `out`
+    const float* merge_lse;   // its per-row log-sum-exp
+    int32_t interleave;       // striping of the current tokens over ranks
+    int32_t pcp;
+    // Split history (overlap kernel, SPLIT): the table entries are cut into
+    // `splits` equal ranges, one per workgroup of a row tile; each writes its
+    // normalised FP32 partial output and log-sum-exp, merged afterwards.
+    int32_t splits;
+    float* part_o;            // [splits, pcp * Hq * local_q, D]
+    float* part_lse;          // [splits, pcp * Hq * local_q]
+};
+
+// ln(E[(1 + f) / 2^f]) for f uniform in [0, 1): how much the linear-mantissa
+// exp2 of the FP8 overlap kernel overestimates a sum of exponentials on
+// average (1.04069); subtracted from that kernel's log-sum-exp outputs.
+constexpr float kFastLseBias = 0.03987f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+    return __uint_as_float(bits16 << 16);
+}
+
+// Max / sum of a value over lanes l and l^32 (the two k-groups of a 32x32
+// MFMA tile, which hold different keys of the same query).
+__device__ __forceinline__ float halves_max(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Key (within the 64-key tile) held by accumulator register r of score tile t
+// in lane half h.  The 32x32 accumulator puts row 8*(r/4) + 4*h + r%4 in
+// register r; K rows are ordered so that P^T comes out in PV B-operand order:
+//   FP8 (one PV MFMA eats 64 keys, 32 per lane half): key = 32h + 16t + r
+//   BF16 (one PV MFMA eats 16 keys, 8 per lane half):
+//        key = 32t + 16*(r/8) + 8h + r%8
+template <bool FP8>
+__device__ __forceinline__ int key_of_acc(int t, int r, int h) {
+    return FP8 ? 32 * h + 16 * t + r : 32 * t + 16 * (r >> 3) + 8 * h + (r & 7);
+}
+// Same map indexed by the A-operand row rho (0..31) of the score MFMA.
+template <bool FP8>
+__device__ __forceinline__ int key_of_row(int t, int rho) {
+    return key_of_acc<FP8>(t, 4 * (rho >> 3) + (rho & 3), (rho >> 2) & 1);
+}
+
+// LDS row holding key `key` of a 64-key tile.  FP8 tiles swap key bits 3
+// and 5: the 16 score-operand rows a 16-lane group reads (keys 32h+16t+r,
+// r < 8) and the 8 keys a transposing V read covers then differ in the low 4
+// row bits, and the per-lane part of every K, V and DMA address is the same
+// for all tiles t, reads s and DMA blocks.  BF16 tiles keep key order.
+template <bool FP8>
+__device__ __forceinline__ int lds_row(int key) {
+    if constexpr (FP8) return (key & ~0x28) | ((key >> 2) & 0x8) | ((key << 2) & 0x20);
+    return key;
+}
+
+// XOR swizzle of the 16-byte chunk index within LDS row `row`, making the
+// score-operand reads (16 rows per 16-lane group) and the transposing V
+// reads (8 rows x 16 bytes, or 4 rows x 32 bytes) bank-conflict free.
+template <bool FP8, int CHUNKS>
+__device__ __forceinline__ int chunk_swizzle(int row) {
+    constexpr int mask = (CHUNKS < 16 ? CHUNKS : 16) - 1;
+    const int s = FP8 ? (row & 15) : (((row & 7) << 1) | ((row >> 3) & 1));
+    return s & mask;
+}
+// FP8 V tiles use an even-only swizzle: the two 16-lane groups of a
+// transposing read that share rows (d halves 2dt and 2dt+1) then land on
+// disjoint chunk sets (even vs odd), so 32 lanes cover all 64 banks once.
+template <bool FP8, int CHUNKS>
+__device__ __forceinline__ int chunk_swizzle_v(int row) {
+    constexpr int mask = (CHUNKS < 16 ? CHUNKS : 16) - 1;
+    if constexpr (FP8) return (2 * row) & mask & 14;
+    return chunk_swizzle<FP8, CHUNKS>(row);
+}
+
+// Four bf16 values (8 bytes) widened exactly from four e4m3 codes (one dword).
+__device__ __forceinline__ v2i e4m3x4_to_bf16x4(int codes) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(codes, false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(codes, true);
+    // e4m3 values are exact in bf16: keep the upper half of each f32.
+    const int w0 = (int)((__float_as_uint(lo[0]) >> 16) | (__float_as_uint(lo[1]) & 0xffff0000u));
+    const int w1 = (int)((__float_as_uint(hi[0]) >> 16) | (__float_as_uint(hi[1]) & 0xffff0000u));
+    return v2i{w0, w1};
+}
+
+// s_waitcnt vmcnt(0) with expcnt/lgkmcnt left unconstrained (gfx9 encoding).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Transposing LDS reads as inline asm.  The builtins carry no memory-operand
+// information, so the compiler orders them after every in-flight LDS DMA,
+// including the prefetch of the *other* buffer, which would serialise the
+// pipeline.  Ordering against this buffer's DMA is provided by the
+// vmcnt(0) + barrier at the top of each tile; lds_results_ready() makes the
+// results usable.  OFF is the instruction's immediate byte offset.
+__device__ __forceinline__ uint32_t lds_address(const uint8_t* p) {
+    return (uint32_t)(uintptr_t)PCPA_LDS(const uint8_t, p);
+}
+template <int OFF>
+__device__ __forceinline__ v2i ds_read_tr8_b64(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+    v2i r;
+    asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+    return r;
+}
+template <int OFF>
+__device__ __forceinline__ v2i ds_read_tr16_b64(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+    v2i r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+    return r;
+}
+// s_waitcnt lgkmcnt(0), with the read results as operands so that no use of
+// them (and no copy of the registers) can be scheduled before the wait.
+__device__ __forceinline__ void lds_results_ready(v2i (&x)[8]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7]));
+}
+__device__ __forceinline__ void lds_results_ready(v2i (&x)[4]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]));
+}
+
+// Position in the walk over the block table: entry e (rank-major (rank,
+// block) order), tile start `base` within the page, the page's valid length
+// n, and the byte offset of this KV head's K block in the pool.
+struct TileCursor {
+    int e;
+    int base;
+    int n;
+    int64_t k_off;
+};
+
+// The tile after `c`: the next 64 keys of the same page, or the first tile
+// of the next table entry with valid tokens and an in-range page.  Entries
+// whose page index is outside [0, num_pages) are never read.  The table and
+// the valid lengths are read-only for the whole launch, so they are read
+// through the constant address space: scalar loads, which do not share the
+// vector-memory counter that the LDS-DMA waits count.
+__device__ __forceinline__ TileCursor next_tile(const FwdArgs& a, int head, TileCursor c) {
+    if (c.base + kKeyTile < c.n) {
+        c.base += kKeyTile;
+        return c;
+    }
+    typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+    const const_i32_ptr table = (const_i32_ptr)a.block_table;
+    const const_i32_ptr lens = (const_i32_ptr)a.page_valid_len;
+    for (int e = c.e + 1; e < a.num_entries; ++e) {
+        const int page = table[e];
+        const int n = min(lens[e], a.block_size);
+        if (n > 0 && (unsigned)page < (unsigned)a.num_pages)
+            return TileCursor{e, 0, n, (int64_t)page * a.page_stride + (int64_t)head * a.head_stride};
+    }
+    return TileCursor{a.num_entries, 0, 0, 0};
+}
+
+// The tile after `c` in the single "page" of the current tokens (CAUSAL
+// kernels): entry 0 holds all block_size current tokens in global order;
+// there is no block table.
+__device__ __forceinline__ TileCursor next_current_tile(const FwdArgs& a, int head, TileCursor c) {
+    if (c.e < 0) return TileCursor{0, 0, a.block_size, (int64_t)head * a.head_stride};
+    if (c.base + kKeyTile < c.n) {
+        c.base += kKeyTile;
+        return c;
+    }
+    return TileCursor{a.num_entries, 0, 0, 0};
+}
+
+}  // namespace pcpa

@@ -1,0 +1,674 @@
+// ovl::history_fwd_overlap: the e4m3 head_dim-256 kernel, and the merge of
+// split-history partial outputs.
+#pragma once
+
+#include "common.hpp"
+
+namespace pcpa {
+
+// ============================================================================
+// Helpers of the overlap kernel below.
+// ============================================================================
+namespace ovl {
+
+// Starting reference max: finite, so that a phantom tile (all scores -inf)
+// gives alpha = exp2(0) = 1 and probabilities of 0, and far below any real
+// score, so that the first real tile gives alpha = 0.
+constexpr float kMaxFloor = -1.0e30f;
+
+// A 16-byte chunk of zeros in global memory: the source of the V rows of a
+// partial tile that lie past its valid length.
+__device__ __attribute__((aligned(16))) uint8_t zero_chunk[16];
+
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+template <int OFF>
+__device__ __forceinline__ v4i ds_read_b128(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+    v4i r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+    return r;
+}
+// s_waitcnt lgkmcnt(N) with the awaited read results as operands, so that
+// no use of them is scheduled before the wait.
+template <int N>
+__device__ __forceinline__ void lds_wait(v4i (&x)[2]) {
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x[0]), "+v"(x[1]) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void lds_wait(v2i (&x)[4]) {
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]) : "i"(N));
+}
+// max(a, b, c) in one v_max3_f32, without the NaN-quieting moves the
+// compiler adds around fmaxf of accumulator reads.  Inputs are scores or
+// -inf, never NaN.
+__device__ __forceinline__ float max3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+// s_waitcnt vmcnt(N), expcnt/lgkmcnt unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmem_le() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// Empty asm statements pin a slice's results where the slice is written:
+// without them the compiler sinks the probabilities (used only in the next
+// iteration) below the PV MFMAs, and nothing overlaps.
+__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin(int& x) { asm volatile("" : "+v"(x)); }
+
+// Scores of keys at or past `valid` become -inf.  Key of accumulator (t, r)
+// in lane half h: 32h + 16t + r (key_of_acc), compared as 16t + r against
+// valid - 32h so that the per-register side is an inline constant.
+__device__ __forceinline__ void mask_tail(v16f (&s)[2], int valid, int h) {
+    const int lim = valid - 32 * h;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if (16 * t + r >= lim) s[t][r] = -INFINITY;
+}
+
+}  // namespace ovl
+
+
+// ============================================================================
+// FP8 kernel with an in-wave MFMA/softmax overlap (head_dim 128 and 256).
+//
+// gfx950 overlaps an MFMA with independent VALU work of the same wave, but a
+// single wave per SIMD issues too slowly to keep the matrix core busy.  So
+// this kernel runs two waves per SIMD (8 waves, 256 query rows per
+// workgroup; every wave sees the same K/V tiles, which halves the LDS-DMA
+// work per row) and splits each wave's tile step into two halves:
+//
+//   S half:   S^T(t) = K(t) Q^T                              (MFMA only)
+//   PV half:  O^T += V^T(t-1) P^T(t-1), interleaved MFMA by MFMA with the
+//             softmax of S(t) -> P(t); then O^T is rescaled if tile t raised
+//             the running max (lazily, so rarely)
+//
+// Waves 0-3 run [S(j) | PV(j-1) + softmax(j)] in iteration j and waves 4-7
+// run [PV(j-2) + softmax(j-1) | S(j)], so that on every SIMD one wave feeds
+// the matrix core alone while the other interleaves its PV MFMAs with its
+// softmax.  One barrier per iteration.  K and V tiles live in separate
+// four-stage LDS rings (tile t in stage t % 4): K(j+2) and V(j+1) are
+// requested at the top of iteration j.  Tiles before the first and after
+// the last are "phantom" tiles without valid keys: their scores are masked
+// to -inf (P = 0, softmax state unchanged, since the running max starts at
+// a finite floor) and their V stages hold zeros (zeroed up front for tiles
+// -2 and -1, loaded from zero_chunk afterwards), so every wave runs the same
+// loop body until the last real PV.  Everything is register resident in 256
+// VGPRs, so the MFMAs write the scores where the softmax reads them.
+// ============================================================================
+namespace ovl {
+
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRowsPerGroup = kWaves * 32;
+constexpr int kStages = 4;
+
+template <int D>
+struct Shape {
+    static_assert(D == 128 || D == 256, "overlap kernel covers head_dim 128 and 256");
+    static constexpr int ROW = D;            // e4m3 bytes of one key row
+    static constexpr int CHUNKS = D / 16;
+    static constexpr int TILE = kKeyTile * ROW;
+    static constexpr int RING = kStages * TILE;
+    static constexpr int QK = D / 64;        // k-steps of the score MFMA
+    static constexpr int NX = 2 * QK;        // score MFMAs per tile
+    static constexpr int DT = D / 32;        // PV MFMAs per tile
+    static constexpr int DPW = TILE / 1024 / kWaves;  // 1 KB DMA blocks per wave per K (or V) tile
+    // DMA block 8i + wave lands 32i LDS rows after block `wave` (rows
+    // < 32): lds_row maps row bit 5 to key bit 3, so its chunk is 8i keys
+    // further on, with the same swizzle.
+    static constexpr int DMA_KEY_STEP = 8;
+    static_assert(DPW == 1 || 8 * 1024 / ROW == 32, "block rows must step by 32");
+    // Softmax micro-slices [pv_begin(i), pv_begin(i+1)) run beside PV MFMA i.
+    static constexpr int pv_begin(int i) {
+        constexpr int b256[] = {0, 4, 6, 7, 8, 9, 10, 11, 14};
+        constexpr int b128[] = {0, 5, 8, 11, 14};
+        return D == 256 ? b256[i] : b128[i];
+    }
+};
+
+struct Lanes {
+    uint32_t k_addr;  // score operand, K stage 0, k-step 0, low 16 bytes
+    uint32_t v_addr;  // PV operand, V stage 0, d tile 0 (includes the ring offset)
+    uint32_t dma_k;   // byte offset of the lane's K chunk of DMA block `wave` in a tile
+    uint32_t dma_v;   // same for V (its own swizzle)
+};
+
+// Tiles j-1 .. j+2 of iteration j.  e < 0: before the first tile;
+// e >= num_entries: after the last (both phantom, valid length 0).
+struct Cursors {
+    TileCursor cm1, c0, c1, c2;
+};
+
+__device__ __forceinline__ bool is_real(const FwdArgs& a, const TileCursor& c) {
+    return c.e >= 0 && c.e < a.num_entries;
+}
+
+// Per-lane online-softmax state (log2 domain) and the scratch of the
+// softmax in progress.  l is the full row sum (both lane halves hold it).
+struct SoftmaxRow {
+    float cscale;   // Q row scale * softmax_scale * k_scale * log2(e)
+    float cscale8;  // 8 * cscale
+    float m;        // reference max the probabilities are taken against
+    float l;        // running sum of the e4m3 probabilities, same reference
+    float alpha;    // rescale factor of the last softmax (1: no change)
+    float mx, m_use, shift;
+};
+
+// Micro-slice K of the online softmax of one score tile s (32 scores per
+// lane, masked keys already -inf), producing P as e4m3 in PV B-operand
+// order.  0-3: running max over 8 scores each; 4: new reference max (it lags
+// the tile max by at most 2.5, so probabilities stay below 2^(6 + 2.5) =
+// 362 < 448) and rescale factor; 5-12: four probabilities each, one dword
+// of P; 13: reference update.  The row sum is taken from P by an MFMA.
+//
+// FAST: P = 2^x (x = s * cscale + 6 - m_use) is produced directly as its
+// e4m3 code round(8x + 56), clamped to [0, 255] by v_cvt_pk_u8_f32.  For
+// x = n + f that code decodes to 2^n (1 + f) rounded to 3 mantissa bits:
+// the exponential is interpolated linearly between powers of two (at most
+// 6.1% high, a shape error of +-3% once normalised), which is the e4m3
+// rounding step of P itself.  Codes below 8 are the e4m3 subnormals of
+// values under 2^-6, i.e. under 2^-14 of the tile max.  Otherwise P =
+// v_exp_f32 rounded by v_cvt_pk_fp8_f32.
+template <int K, bool FAST>
+__device__ __forceinline__ void softmax_slice(const v16f (&s)[2], v8i& p, SoftmaxRow& sm) {
+    if constexpr (K < 4) {
+        constexpr int t = K >> 1, r = 8 * (K & 1);
+        float mx = max3(s[t][r], s[t][r + 1], s[t][r + 2]);
+        mx = max3(mx, s[t][r + 3], s[t][r + 4]);
+        mx = max3(mx, s[t][r + 5], s[t][r + 6]);
+        mx = K == 0 ? max3(mx, s[t][r + 7], s[t][r + 7]) : max3(mx, s[t][r + 7], sm.mx);
+        sm.mx = mx;
+        pin(sm.mx);
+    } else if constexpr (K == 4) {
+        const float mxs = halves_max(sm.mx) * sm.cscale;
+        sm.m_use = fmaxf(sm.m, mxs - 2.5f);
+        sm.alpha = __builtin_amdgcn_exp2f(sm.m - sm.m_use);
+        // FAST: 8x + 56 = s * 8 cscale + (8 (6 - m_use) + 56)
+        sm.shift = FAST ? fmaf(-8.f, sm.m_use, 8.f * kPBiasLog2 + 56.f) : kPBiasLog2 - sm.m_use;
+        pin(sm.m_use);
+        pin(sm.alpha);
+        pin(sm.shift);
+    } else if constexpr (K < 13) {
+        constexpr int w = K - 5, t = w >> 2, r0 = 4 * (w & 3);
+        int word;
+        if constexpr (FAST) {
+            word = __builtin_amdgcn_cvt_pk_u8_f32(fmaf(s[t][r0 + 0], sm.cscale8, sm.shift), 0, 0);
+            word = __builtin_amdgcn_cvt_pk_u8_f32(fmaf(s[t][r0 + 1], sm.cscale8, sm.shift), 1, word);
+            word = __builtin_amdgcn_cvt_pk_u8_f32(fmaf(s[t][r0 + 2], sm.cscale8, sm.shift), 2, word);
+            word = __builtin_amdgcn_cvt_pk_u8_f32(fmaf(s[t][r0 + 3], sm.cscale8, sm.shift), 3, word);
+        } else {
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(s[t][r0 + 0], sm.cscale, sm.shift));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(s[t][r0 + 1], sm.cscale, sm.shift));
+            const float p2 = __builtin_amdgcn_exp2f(fmaf(s[t][r0 + 2], sm.cscale, sm.shift));
+            const float p3 = __builtin_amdgcn_exp2f(fmaf(s[t][r0 + 3], sm.cscale, sm.shift));
+            // The first convert's untouched high half is overwritten by the
+            // second, so any register serves as its "old" operand.
+            const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(p0, p1, __float_as_int(p0), false);
+            word = __builtin_amdgcn_cvt_pk_fp8_f32(p2, p3, pk, true);
+        }
+        pin(word);
+        p[w] = word;
+    } else {
+        sm.m = sm.m_use;
+        pin(sm.m);
+    }
+}
+
+template <int LO, int HI, bool FAST>
+__device__ __forceinline__ void softmax_slices(const v16f (&s)[2], v8i& p, SoftmaxRow& sm) {
+    if constexpr (LO < HI) {
+        softmax_slice<LO, FAST>(s, p, sm);
+        softmax_slices<LO + 1, HI, FAST>(s, p, sm);
+    }
+}
+
+// Key of the lane's chunk of DMA block i (LDS byte (8i + wave) * 1024 +
+// 16 * lane, rows permuted by lds_row).
+template <class S>
+__device__ __forceinline__ int dma_chunk_key(int i, int wave_off) {
+    return lds_row<true>((i * kWaves * 1024 + wave_off + __lane_id() * 16) / S::ROW);
+}
+
+// Issue the K tile of cursor c into K stage st.  (Pointers are formed in
+// plain variables: address-space casts of expressions that depend on S trip
+// the host compilation pass.)
+template <class S>
+__device__ __forceinline__ void load_k(const FwdArgs& a, const TileCursor& c, uint8_t* lds, int st, int wave_off,
+                                       uint32_t off) {
+    const uint8_t* const kt = a.kv + c.k_off + (int64_t)c.base * S::ROW + off;
+    uint8_t* const dst = lds + st * S::TILE + wave_off;
+#pragma unroll
+    for (int i = 0; i < S::DPW; ++i) {
+        const uint8_t* const src = kt + i * S::DMA_KEY_STEP * S::ROW;
+        uint8_t* const d = dst + i * (kWaves * 1024);
+        __builtin_amdgcn_global_load_lds(src, PCPA_LDS(void, d), 16, 0, 0);
+    }
+}
+
+// Issue the V tile of cursor c into V stage st.  Rows past the valid length
+// (all rows of a phantom tile) come from zero_chunk, so V stages of masked
+// keys hold zeros and the number of loads per tile never changes.
+template <class S>
+__device__ __forceinline__ void load_v(const FwdArgs& a, const TileCursor& c, uint8_t* lds, int st, int wave_off,
+                                       uint32_t off, bool real) {
+    const uint8_t* const vt =
+        a.kv + c.k_off + (int64_t)c.base * S::ROW + (int64_t)a.num_kv_heads * a.head_stride + off;
+    uint8_t* const dst = lds + S::RING + st * S::TILE + wave_off;
+    const int valid = real ? c.n - c.base : 0;
+    if (valid >= kKeyTile) {
+#pragma unroll
+        for (int i = 0; i < S::DPW; ++i) {
+            const uint8_t* const src = vt + i * S::DMA_KEY_STEP * S::ROW;
+            uint8_t* const d = dst + i * (kWaves * 1024);
+            __builtin_amdgcn_global_load_lds(src, PCPA_LDS(void, d), 16, 0, 0);
+        }
+    } else {
+        const uint8_t* const zero = zero_chunk;
+#pragma unroll
+        for (int i = 0; i < S::DPW; ++i) {
+            const uint8_t* const src =
+                dma_chunk_key<S>(i, wave_off) < valid ? vt + i * S::DMA_KEY_STEP * S::ROW : zero;
+            uint8_t* const d = dst + i * (kWaves * 1024);
+            __builtin_amdgcn_global_load_lds(src, PCPA_LDS(void, d), 16, 0, 0);
+        }
+    }
+}
+
+// S half: S^T = K Q^T from K stage KST; operand reads one MFMA ahead (the
+// other wave on the SIMD covers the latency).  PREFETCH_V: the last slot
+// starts the first V-operand read of the PV half that follows (stage VST).
+// Also adds to l the row sum of P_last, the probabilities the preceding PV
+// half consumed, scaled by the alpha that PV half applied.
+template <int D, int KST, bool PREFETCH_V, int VST>
+__device__ __forceinline__ void s_half(uint32_t k_addr, uint32_t v_addr, const v8i (&q)[Shape<D>::QK], v16f (&s)[2],
+                                       v2i (&xv)[4], const v8i& p_last, SoftmaxRow& sm) {
+    using S = Shape<D>;
+    // ones (e4m3 1.0) x P_last puts sum_k P_last[k][q] in every accumulator
+    // of query column q.  The ones operand is rebuilt from an opaque register
+    // instead of occupying 8 VGPRs for good.
+    int one = 0x38383838;
+    asm volatile("" : "+v"(one));
+    const v8i ones = {one, one, one, one, one, one, one, one};
+    v16f rowsum = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, p_last, v16f{}, 0, 0, 0, 0, 0, 0);
+    v4i kr[2][2];
+    auto issue_k = [&](auto oc) {
+        constexpr int op = decltype(oc)::value, c = op >> 1, t = op & 1;
+        constexpr int off = KST * S::TILE + t * 16 * S::ROW;
+        kr[op & 1][0] = ds_read_b128<off>(k_addr ^ ((4 * c) << 4));
+        kr[op & 1][1] = ds_read_b128<off>(k_addr ^ ((4 * c + 1) << 4));
+    };
+    issue_k(std::integral_constant<int, 0>{});
+    static_for<0, S::NX>([&](auto oc) {
+        constexpr int op = decltype(oc)::value, c = op >> 1, t = op & 1;
+        lds_wait<0>(kr[op & 1]);
+        if constexpr (op + 1 < S::NX) {
+            issue_k(std::integral_constant<int, op + 1>{});
+        } else if constexpr (PREFETCH_V) {
+            // keys 32g + 8s + m of the d tile live in LDS rows (8g + m) + {0, 32, 16, 48}[s]
+            constexpr int off = VST * S::TILE;
+            xv[0] = ds_read_tr8_b64<off + 0 * S::ROW>(v_addr);
+            xv[1] = ds_read_tr8_b64<off + 32 * S::ROW>(v_addr);
+            xv[2] = ds_read_tr8_b64<off + 16 * S::ROW>(v_addr);
+            xv[3] = ds_read_tr8_b64<off + 48 * S::ROW>(v_addr);
+        }
+        const v4i lo = kr[op & 1][0], hi = kr[op & 1][1];
+        const v8i kop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        s[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kop, q[c], c == 0 ? v16f{} : s[t], 0, 0, 0, 0, 0, 0);
+    });
+    // All 16 row-sum registers stay allocated until here: the inline-asm LDS
+    // reads above are invisible to the hazard checks and must not be given
+    // registers that the in-flight MFMA is still going to write.
+    asm volatile("" : "+v"(rowsum));
+    sm.l = fmaf(rowsum[0], sm.alpha, sm.l);
+}
+
+// PV half: O^T += V^T P_old^T from V stage VST, beside the softmax of s
+// (valid keys < valid) into p_new; then the lazy O^T rescale.  PREFETCHED:
+// the first V-operand read was issued by the S half.
+template <int D, int VST, bool PREFETCHED, bool FAST>
+__device__ __forceinline__ void pv_half(uint32_t v_addr, v2i (&xv0)[4], v16f (&o)[Shape<D>::DT], const v8i& p_old,
+                                        v16f (&s)[2], v8i& p_new, SoftmaxRow& sm, int valid, int h) {
+    using S = Shape<D>;
+    if (valid < kKeyTile) mask_tail(s, valid, h);
+    v2i xv1[4];
+    auto buf = [&](auto dc) -> v2i(&)[4] {
+        if constexpr ((decltype(dc)::value & 1) == 0)
+            return xv0;
+        else
+            return xv1;
+    };
+    auto issue_v = [&](auto dc) {
+        constexpr int dt = decltype(dc)::value;
+        constexpr int off = VST * S::TILE;
+        const uint32_t addr = v_addr ^ ((2 * dt) << 4);
+        v2i(&x)[4] = buf(dc);
+        x[0] = ds_read_tr8_b64<off + 0 * S::ROW>(addr);
+        x[1] = ds_read_tr8_b64<off + 32 * S::ROW>(addr);
+        x[2] = ds_read_tr8_b64<off + 16 * S::ROW>(addr);
+        x[3] = ds_read_tr8_b64<off + 48 * S::ROW>(addr);
+    };
+    if constexpr (!PREFETCHED) issue_v(std::integral_constant<int, 0>{});
+    static_for<0, S::DT>([&](auto dc) {
+        constexpr int dt = decltype(dc)::value;
+        v2i(&x)[4] = buf(dc);
+        lds_wait<0>(x);
+        if constexpr (dt + 1 < S::DT) issue_v(std::integral_constant<int, dt + 1>{});
+        const v8i vop = {x[0][0], x[0][1], x[1][0], x[1][1], x[2][0], x[2][1], x[3][0], x[3][1]};
+        o[dt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vop, p_old, o[dt], 0, 0, 0, 0, 0, 0);
+        softmax_slices<S::pv_begin(dt), S::pv_begin(dt + 1), FAST>(s, p_new, sm);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    // O^T gained P_old's tile; both O^T and l move to the new reference (l
+    // gains P_old's row sum, times this alpha, in the next S half).
+    sm.l *= sm.alpha;
+    if (__builtin_amdgcn_ballot_w64(sm.alpha < 1.f) != 0) {
+#pragma unroll
+        for (int dt = 0; dt < S::DT; ++dt) o[dt] *= sm.alpha;
+    }
+}
+
+// Iteration j, J4 = j mod 4; LATE: waves 4-7 (PV half first, one tile behind).
+template <int D, int J4, bool LATE, bool FAST>
+__device__ __forceinline__ void iteration(const FwdArgs& a, uint8_t* lds, int wave, int h, const Lanes& L,
+                                          const v8i (&q)[Shape<D>::QK], v16f (&s)[2], v8i (&pbuf)[2],
+                                          v16f (&o)[Shape<D>::DT], SoftmaxRow& sm, Cursors& cs, int head) {
+    using S = Shape<D>;
+    constexpr int KST = J4;  // K(j)
+
+    // ---- K(j) and V(j-1) have landed (for every wave) ----------------------
+    // Loads issued one iteration ago may be pending: V(j), and K(j+1) if tile
+    // j+1 is real.
+    if (is_real(a, cs.c1))
+        wait_vmem_le<2 * S::DPW>();
+    else
+        wait_vmem_le<S::DPW>();
+    __builtin_amdgcn_s_barrier();
+    // K stage (j+2) % 4 held K(j-2) and V stage (j+1) % 4 held V(j-3); both
+    // were last read in iteration j-1.  The wave offset and operand bases
+    // are made opaque so that the DMA destinations and operand addresses are
+    // recomputed in the loop rather than hoisted and spilled.
+    int wave_off = wave * 1024;
+    uint32_t k_addr = L.k_addr, v_addr = L.v_addr;
+    asm volatile("" : "+s"(wave_off), "+v"(k_addr), "+v"(v_addr));
+    if (is_real(a, cs.c2)) load_k<S>(a, cs.c2, lds, (J4 + 2) % kStages, wave_off, L.dma_k);
+    load_v<S>(a, cs.c1, lds, (J4 + 1) % kStages, wave_off, L.dma_v, is_real(a, cs.c1));
+
+    v2i xv[4];
+    if constexpr (!LATE) {
+        // S(j), then PV(j-1) beside softmax(j)
+        constexpr int VST = (J4 + 3) % kStages;
+        s_half<D, KST, true, VST>(k_addr, v_addr, q, s, xv, pbuf[J4 & 1], sm);
+        pv_half<D, VST, true, FAST>(v_addr, xv, o, pbuf[(J4 + 1) & 1], s, pbuf[J4 & 1], sm,
+                              is_real(a, cs.c0) ? cs.c0.n - cs.c0.base : 0, h);
+    } else {
+        // PV(j-2) beside softmax(j-1), then S(j)
+        constexpr int VST = (J4 + 2) % kStages;
+        pv_half<D, VST, false, FAST>(v_addr, xv, o, pbuf[J4 & 1], s, pbuf[(J4 + 1) & 1], sm,
+                               is_real(a, cs.cm1) ? cs.cm1.n - cs.cm1.base : 0, h);
+        s_half<D, KST, false, 0>(k_addr, v_addr, q, s, xv, pbuf[J4 & 1], sm);
+    }
+
+    cs.cm1 = cs.c0;
+    cs.c0 = cs.c1;
+    cs.c1 = cs.c2;
+    if (is_real(a, cs.c2)) cs.c2 = next_tile(a, head, cs.c2);
+}
+
+// The loop of one wave group; iteration j runs while j <= T + 1 (T tiles).
+template <int D, bool LATE, bool FAST>
+__device__ __forceinline__ void walk(const FwdArgs& a, uint8_t* lds, int wave, int h, const Lanes& L,
+                                     const v8i (&q)[Shape<D>::QK], v16f (&s)[2], v8i (&pbuf)[2],
+                                     v16f (&o)[Shape<D>::DT], SoftmaxRow& sm, Cursors cs, int head) {
+    for (;;) {
+        // after iteration j the loop ends if tile j-1 was past the last tile
+        bool done = cs.cm1.e >= a.num_entries;
+        iteration<D, 0, LATE, FAST>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+        if (done) break;
+        done = cs.cm1.e >= a.num_entries;
+        iteration<D, 1, LATE, FAST>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+        if (done) break;
+        done = cs.cm1.e >= a.num_entries;
+        iteration<D, 2, LATE, FAST>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+        if (done) break;
+        done = cs.cm1.e >= a.num_entries;
+        iteration<D, 3, LATE, FAST>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+        if (done) break;
+    }
+}
+
+// LSE: also write each row's log-sum-exp (a separate instantiation, so that
+// the plain one keeps its register allocation).
+// SPLIT: the workgroup walks only its split's share of the table entries
+// and writes a normalised FP32 partial output and log-sum-exp (merged by
+// merge_splits_kernel).
+template <int D, bool FAST, bool LSE, bool SPLIT = false>
+__global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
+    using S = Shape<D>;
+    constexpr int QK = S::QK, DT = S::DT, ROW = S::ROW, CHUNKS = S::CHUNKS;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * S::RING];
+
+    // ---- XCD-aware work mapping (as history_fwd_kernel) ---------------------
+    // Items run row tile fastest, so an XCD's workgroups share one (KV head,
+    // split) and with it the pages they stream.
+    const int splits = SPLIT ? a.splits : 1;
+    const int items = a.row_tiles * a.num_kv_heads * splits;
+    const int per_xcd = (items + 7) / 8;
+    const int item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (item >= items) return;
+    const int row_tile = item % a.row_tiles;
+    const int head = item / a.row_tiles / splits;
+    const int split = item / a.row_tiles - head * splits;
+    int entry_begin = 0;
+    if constexpr (SPLIT) {
+        entry_begin = (int)((int64_t)a.num_entries * split / splits);
+        a.num_entries = (int)((int64_t)a.num_entries * (split + 1) / splits);
+    }
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 31;
+    const int h = lane >> 5;
+    const int grp = lane >> 4;
+    const int gl = lane & 15;
+
+    // ---- this lane's query row and its e4m3 Q^T operand ---------------------
+    const int row = row_tile * kRowsPerGroup + wave * 32 + j;
+    const bool row_ok = row < a.rows_per_head;
+    const int rowc = row_ok ? row : a.rows_per_head - 1;
+    const int rank = rowc / a.group_rows;
+    const int rem = rowc - rank * a.group_rows;
+    const int head_in_group = rem / a.local_q;
+    const int tok = rem - head_in_group * a.local_q;
+    const int64_t row_off =
+        ((int64_t)(rank * a.num_q_heads + head * a.group + head_in_group) * a.local_q + tok) * D * 2;
+    const uint8_t* const qrow = a.q + row_off;
+
+    v8i q[QK];
+    SoftmaxRow sm;
+    {
+        // lane (j, h) holds d = 64c + 32h + [0, 32) of its row, as e4m3.
+        float amax = 0.f;
+#pragma unroll
+        for (int c = 0; c < QK; ++c)
+#pragma unroll
+            for (int part = 0; part < 4; ++part) {
+                const v4i raw = *(const v4i*)(qrow + (64 * c + 32 * h) * 2 + 16 * part);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const uint32_t u = (uint32_t)raw[w];
+                    amax = fmaxf(amax, fabsf(bf16_bits_to_f32(u & 0xffffu)));
+                    amax = fmaxf(amax, fabsf(bf16_bits_to_f32(u >> 16)));
+                }
+            }
+        amax = halves_max(amax);
+        const float inv = amax > 0.f ? kFp8Max / amax : 1.f;
+        const float sigma = amax > 0.f ? amax / kFp8Max : 1.f;
+#pragma unroll
+        for (int c = 0; c < QK; ++c)
+#pragma unroll
+            for (int part = 0; part < 4; ++part) {
+                const v4i raw = *(const v4i*)(qrow + (64 * c + 32 * h) * 2 + 16 * part);
+#pragma unroll
+                for (int w = 0; w < 2; ++w) {
+                    const uint32_t u0 = (uint32_t)raw[2 * w], u1 = (uint32_t)raw[2 * w + 1];
+                    int pk = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_bits_to_f32(u0 & 0xffffu) * inv,
+                                                             bf16_bits_to_f32(u0 >> 16) * inv, 0, false);
+                    pk = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_bits_to_f32(u1 & 0xffffu) * inv,
+                                                         bf16_bits_to_f32(u1 >> 16) * inv, pk, true);
+                    q[c][2 * part + w] = pk;
+                }
+            }
+        sm.cscale = sigma * a.score_scale;
+        sm.cscale8 = 8.f * sm.cscale;
+        sm.m = kMaxFloor;
+        sm.l = 0.f;
+        sm.alpha = 1.f;
+    }
+
+    // ---- lane constants ------------------------------------------------------
+    Lanes L;
+    {
+        const uint32_t base = lds_address(lds);
+        const int krow = lds_row<true>(key_of_row<true>(0, j));
+        L.k_addr = base + krow * ROW + (((2 * h) ^ chunk_swizzle<true, CHUNKS>(krow)) << 4);
+        // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1): key 32*(grp>>1) + (gl>>1)
+        const int vrow = lds_row<true>(32 * (grp >> 1) + (gl >> 1));
+        L.v_addr = base + S::RING + vrow * ROW + (((grp & 1) ^ chunk_swizzle_v<true, CHUNKS>(vrow)) << 4) +
+                   8 * (gl & 1);
+        // DMA block `wave` lands at LDS byte wave * 1024 + 16 * lane.
+        const int byte = wave * 1024 + lane * 16;
+        const int drow = byte / ROW;
+        const int pos = (byte % ROW) / 16;
+        const int key = lds_row<true>(drow);
+        L.dma_k = key * ROW + (pos ^ chunk_swizzle<true, CHUNKS>(drow)) * 16;
+        L.dma_v = key * ROW + (pos ^ chunk_swizzle_v<true, CHUNKS>(drow)) * 16;
+    }
+
+    v16f o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = v16f{};
+    v16f s[2];
+    v8i pbuf[2] = {v8i{}, v8i{}};
+
+    // ---- pipeline --------------------------------------------------------------
+    const TileCursor first = next_tile(a, head, TileCursor{entry_begin - 1, 0, 0, 0});
+    if (is_real(a, first)) {
+        // V stages 2 and 3 stand for tiles -2 and -1: zeros.
+        for (int idx = tid; idx < 2 * S::TILE / 16; idx += kThreads)
+            *(v4i*)(lds + S::RING + 2 * S::TILE + 16 * idx) = v4i{0, 0, 0, 0};
+        __syncthreads();
+        const TileCursor before{-1, 0, 0, 0};
+        Cursors cs;
+        cs.cm1 = before;
+        cs.c0 = first;
+        cs.c1 = next_tile(a, head, first);
+        cs.c2 = is_real(a, cs.c1) ? next_tile(a, head, cs.c1) : cs.c1;
+        // K(0), then V(0) and K(1) as if requested at the top of iteration -1.
+        load_k<S>(a, cs.c0, lds, 0, wave * 1024, L.dma_k);
+        load_v<S>(a, cs.c0, lds, 0, wave * 1024, L.dma_v, true);
+        if (is_real(a, cs.c1)) load_k<S>(a, cs.c1, lds, 1, wave * 1024, L.dma_k);
+        if (wave < kWaves / 2)
+            walk<D, false, FAST>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+        else
+            walk<D, true, FAST>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+    }
+
+    // ---- epilogue: O = O^T / l, bf16; log-sum-exp ---------------------------
+    const float scale = sm.l > 0.f ? a.v_scale / sm.l : 0.f;
+    // sum_k exp(score_k) = l * 2^(m - 6), less the average overestimate of
+    // the linear-mantissa exp2
+    const float lse =
+        sm.l > 0.f ? __logf(sm.l) + (sm.m - kPBiasLog2) * kLn2 - (FAST ? kFastLseBias : 0.f) : -INFINITY;
+    if constexpr (SPLIT) {
+        if (row_ok) {
+            const int64_t prow = (int64_t)split * a.rows_per_head * a.num_kv_heads + row_off / (D * 2);
+            float* const po = a.part_o + prow * D;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int d = 32 * dt + 8 * r4 + 4 * h;
+                    *(v4f*)(po + d) = v4f{o[dt][4 * r4 + 0] * scale, o[dt][4 * r4 + 1] * scale,
+                                          o[dt][4 * r4 + 2] * scale, o[dt][4 * r4 + 3] * scale};
+                }
+            if (h == 0) a.part_lse[prow] = lse;
+        }
+        return;
+    }
+    if (LSE && row_ok && h == 0) a.lse[row_off / (D * 2)] = lse;
+    if (row_ok) {
+        uint8_t* const orow = a.out + row_off;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int d = 32 * dt + 8 * r4 + 4 * h;
+                const __bf16 v0 = (__bf16)(o[dt][4 * r4 + 0] * scale);
+                const __bf16 v1 = (__bf16)(o[dt][4 * r4 + 1] * scale);
+                const __bf16 v2 = (__bf16)(o[dt][4 * r4 + 2] * scale);
+                const __bf16 v3 = (__bf16)(o[dt][4 * r4 + 3] * scale);
+                const uint32_t w0 = (uint32_t)__builtin_bit_cast(uint16_t, v0) |
+                                    ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16);
+                const uint32_t w1 = (uint32_t)__builtin_bit_cast(uint16_t, v2) |
+                                    ((uint32_t)__builtin_bit_cast(uint16_t, v3) << 16);
+                *(v2i*)(orow + 2 * d) = v2i{(int)w0, (int)w1};
+            }
+    }
+}
+
+}  // namespace ovl
+
+// Merge of split partial outputs by log-sum-exp: one thread per (row, 8
+// consecutive d).  out = sum_s w_s O_s / sum_s w_s with w_s = e^(lse_s - max),
+// bf16; lse (optional) = max + ln(sum_s w_s).  HBM bound: 4 * D + 4 bytes read
+// per row and split, 2 * D written.
+__global__ void __launch_bounds__(256) merge_splits_kernel(const float* part_o, const float* part_lse, int splits,
+                                                           int64_t rows, int d_vec8, uint8_t* out, float* lse_out) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * d_vec8) return;
+    const int64_t row = idx / d_vec8;
+    const int d0 = (int)(idx - row * d_vec8) * 8;
+    const int D = d_vec8 * 8;
+    float mx = -INFINITY;
+    for (int sp = 0; sp < splits; ++sp) mx = fmaxf(mx, part_lse[sp * rows + row]);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float wsum = 0.f;
+    for (int sp = 0; sp < splits; ++sp) {
+        const float l = part_lse[sp * rows + row];
+        if (l == -INFINITY) continue;
+        const float w = __expf(l - mx);
+        wsum += w;
+        const float* const src = part_o + (sp * rows + row) * D + d0;
+        const v4f lo = *(const v4f*)src, hi = *(const v4f*)(src + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc[i] = fmaf(w, lo[i], acc[i]);
+            acc[4 + i] = fmaf(w, hi[i], acc[4 + i]);
+        }
+    }
+    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+    uint32_t wv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const __bf16 x0 = (__bf16)(acc[2 * i] * inv), x1 = (__bf16)(acc[2 * i + 1] * inv);
+        wv[i] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
+    }
+    *(v4i*)(out + (row * D + d0) * 2) = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
+    if (lse_out && d0 == 0) lse_out[row] = wsum > 0.f ? mx + __logf(wsum) : -INFINITY;
+}
+
+}  // namespace pcpa

@@ -1,0 +1,551 @@
+// history_fwd_kernel: the tile kernel for every head dim and precision, and
+// (CAUSAL) the current-token step.
+#pragma once
+
+#include "common.hpp"
+
+namespace pcpa {
+
+// STORE8: the cache holds e4m3 (else bf16).  FP8: the MFMAs run on e4m3
+// operands (requires STORE8); otherwise they run on bf16, and an e4m3 cache
+// is widened to bf16 while it is staged into LDS.
+template <int D, bool STORE8, bool FP8>
+struct TileShape {
+    static_assert(STORE8 || !FP8, "e4m3 MFMAs need an e4m3 cache");
+    static constexpr int ES = FP8 ? 1 : 2;
+    static constexpr bool F8 = FP8;
+    static constexpr int ROW = D * ES;                 // LDS bytes of one key row
+    static constexpr int CHUNKS = ROW / 16;
+    static constexpr int TILE = kKeyTile * ROW;        // LDS bytes of one K (or V) tile
+    static constexpr int GROW = D * (STORE8 ? 1 : 2);  // cache bytes of one key row
+    static constexpr int GCHUNKS = GROW / 16;
+    static constexpr bool WIDEN = STORE8 && !FP8;
+    // Double-buffered (prefetching) when both buffers fit the 64 KB static
+    // LDS limit; the widening path stages synchronously through registers.
+    static constexpr int NBUF = (!WIDEN && 4 * TILE <= 65536) ? 2 : 1;
+    static constexpr int QK = FP8 ? D / 64 : D / 16;   // k-steps of the score MFMA
+    static constexpr int DT = D / 32;                  // 32-row d tiles of O^T
+    static constexpr int DMA_PER_WAVE = CHUNKS / 4;    // 1 KB DMA blocks per wave per operand
+    // Wave w loads DMA blocks 4i + w.  Block i's lane chunk sits DMA_ROW_DELTA(i)
+    // key rows after block 0's, with the same chunk swizzle, except for 512-byte
+    // rows (bf16 D=256) whose swizzle changes between blocks: those keep one
+    // offset per block (DMA_SPLIT).
+    static constexpr bool DMA_SPLIT = ROW == 512;
+    static constexpr int K_T1_ROWS = FP8 ? 16 : 32;    // LDS rows from score tile 0 to tile 1
+    static constexpr int dma_key_delta(int i) {
+        // keys between DMA block i's lane chunk and block 0's (rows are 4i*1024/ROW apart)
+        return FP8 ? (ROW == 256 ? 16 * (i & 1) + 8 * (i >> 1) : ROW == 128 ? 8 * i : 0) : i * 4096 / ROW;
+    }
+    // Lazy rescale: the running max is only raised when a tile's max exceeds
+    // it by more than this (log2 units); FP8 probabilities then stay below
+    // 2^(kPBiasLog2 + 2.5) = 362 < 448.
+    static constexpr float RESCALE_LOG2 = FP8 ? 2.5f : 8.0f;
+};
+
+// Per-lane constants of the main loop (LDS offsets are within one buffer).
+template <class S>
+struct LaneMap {
+    uint32_t k_addr;                      // score A operand of tile 0 (tile 1: + K_T1_ROWS rows)
+    uint32_t v_addr[S::ES == 1 ? 1 : 2];  // PV A operand base(s)
+    uint32_t dma_off[S::DMA_SPLIT ? S::DMA_PER_WAVE : 1];   // global byte offset of the lane's K DMA chunk
+    uint32_t dma_off_v[S::DMA_SPLIT ? S::DMA_PER_WAVE : 1]; // same for the V tile (its own swizzle)
+};
+
+// Issue asynchronous global->LDS loads of one 64-key K tile and V tile.  The
+// tile is split into 1 KB blocks; each wave loads DMA_PER_WAVE blocks of
+// each, one 16-byte chunk per lane, landing at block + 16 * lane.  The
+// lane's global chunk (dma_off) is chosen so that the swizzled LDS layout
+// comes out.
+template <class S, int BUF>
+__device__ __forceinline__ void stage_tile_async(const FwdArgs& a, const TileCursor& c, uint8_t* lds, int wave,
+                                                 const LaneMap<S>& L) {
+    const uint8_t* const kt = a.kv + c.k_off + (int64_t)c.base * S::GROW;
+    const uint8_t* const vt = kt + (int64_t)a.num_kv_heads * a.head_stride;
+    uint8_t* const lk = lds + BUF * 2 * S::TILE;
+#pragma unroll
+    for (int i = 0; i < S::DMA_PER_WAVE; ++i) {
+        const int block = 4 * i + wave;
+        const uint32_t koff = L.dma_off[S::DMA_SPLIT ? i : 0];
+        const uint32_t voff = L.dma_off_v[S::DMA_SPLIT ? i : 0];
+        const int delta = S::DMA_SPLIT ? 0 : S::dma_key_delta(i) * S::GROW;
+        __builtin_amdgcn_global_load_lds(kt + delta + koff, PCPA_LDS(void, lk + block * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vt + delta + voff, PCPA_LDS(void, lk + S::TILE + block * 1024), 16, 0, 0);
+    }
+}
+
+// Synchronous staging through registers into buffer 0, widening e4m3 to
+// bf16 when the MFMAs are bf16.  Rows at or beyond `valid` get zero V.
+template <class S>
+__device__ __forceinline__ void stage_tile_sync(const FwdArgs& a, const TileCursor& c, int valid, uint8_t* lds,
+                                                int tid) {
+    constexpr int LOADS = kKeyTile * S::GROW / (16 * kThreads);
+    static_assert((kKeyTile * S::GROW) % (16 * kThreads) == 0, "tile must split into 16-byte chunks per thread");
+    const uint8_t* const kpage = a.kv + c.k_off;
+    const uint8_t* const vpage = kpage + (int64_t)a.num_kv_heads * a.head_stride;
+    uint8_t* const lds_k = lds;
+    uint8_t* const lds_v = lds + S::TILE;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int chunk_id = tid + kThreads * i;
+        const int key = chunk_id / S::GCHUNKS;
+        const int ch = chunk_id - key * S::GCHUNKS;
+        const int64_t goff = (int64_t)(c.base + key) * S::GROW + ch * 16;
+        const v4i kc = *(const v4i*)(kpage + goff);
+        v4i vc = *(const v4i*)(vpage + goff);
+        if (key >= valid) vc = v4i{0, 0, 0, 0};
+        const int row = lds_row<S::ES == 1>(key);
+        const int sw = chunk_swizzle<S::ES == 1, S::CHUNKS>(row);
+        const int swv = chunk_swizzle_v<S::ES == 1, S::CHUNKS>(row);
+        if constexpr (S::WIDEN) {
+            // 16 e4m3 codes become 32 bytes (LDS chunks 2ch, 2ch+1).
+            const v2i k0 = e4m3x4_to_bf16x4(kc[0]), k1 = e4m3x4_to_bf16x4(kc[1]);
+            const v2i k2 = e4m3x4_to_bf16x4(kc[2]), k3 = e4m3x4_to_bf16x4(kc[3]);
+            const v2i v0 = e4m3x4_to_bf16x4(vc[0]), v1 = e4m3x4_to_bf16x4(vc[1]);
+            const v2i v2 = e4m3x4_to_bf16x4(vc[2]), v3 = e4m3x4_to_bf16x4(vc[3]);
+            const int lo = row * S::ROW + (((2 * ch) ^ sw) << 4);
+            const int hi = row * S::ROW + (((2 * ch + 1) ^ sw) << 4);
+            *(v4i*)(lds_k + lo) = v4i{k0[0], k0[1], k1[0], k1[1]};
+            *(v4i*)(lds_k + hi) = v4i{k2[0], k2[1], k3[0], k3[1]};
+            *(v4i*)(lds_v + lo) = v4i{v0[0], v0[1], v1[0], v1[1]};
+            *(v4i*)(lds_v + hi) = v4i{v2[0], v2[1], v3[0], v3[1]};
+        } else {
+            *(v4i*)(lds_k + row * S::ROW + ((ch ^ sw) << 4)) = kc;
+            *(v4i*)(lds_v + row * S::ROW + ((ch ^ swv) << 4)) = vc;
+        }
+    }
+}
+
+// Zero V rows [valid, 64) of a staged tile, so that masked (probability 0)
+// keys cannot inject NaN bit patterns from unused cache slots.
+template <class S>
+__device__ __forceinline__ void zero_masked_v(uint8_t* lds_v, int valid, int tid) {
+    for (int idx = tid; idx < (kKeyTile - valid) * S::CHUNKS; idx += kThreads) {
+        const int key = valid + idx / S::CHUNKS;
+        *(v4i*)(lds_v + lds_row<S::ES == 1>(key) * S::ROW + (idx % S::CHUNKS) * 16) = v4i{0, 0, 0, 0};
+    }
+}
+
+// Online-softmax state of one lane: running max (log2 domain, times the
+// lane's score factor), this lane half's share of the running sum, and the
+// O^T accumulator tiles.
+template <class S>
+struct SoftmaxState {
+    float m;
+    float l;
+    v16f o[S::DT];
+};
+
+template <class S>
+using QOperand = typename std::conditional<S::ES == 1, v8i, v8bf>::type;
+
+// One 64-key tile held in LDS buffer BUF: S^T = K Q^T, masked online
+// softmax, O^T += V^T P^T.
+// CAUSAL: `valid` differs per lane (the row's causal limit within the tile,
+// possibly <= 0).
+template <class S, int BUF, bool CAUSAL = false>
+__device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, const QOperand<S> (&qop)[S::QK],
+                                             float cscale, const LaneMap<S>& L, int h, SoftmaxState<S>& st) {
+    constexpr bool FP8 = S::ES == 1;
+    constexpr int ROW = S::ROW, QK = S::QK, DT = S::DT;
+    constexpr int KBASE = BUF * 2 * S::TILE;
+    constexpr int VBASE = KBASE + S::TILE;
+    const uint8_t* const lk = lds + KBASE;
+
+    // ---- S^T = K . Q^T : two 32-key x 32-query tiles --------------------
+    v16f s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        s[t] = v16f{};
+#pragma unroll
+        for (int c = 0; c < QK; ++c) {
+            const uint8_t* const kt = lk + t * S::K_T1_ROWS * ROW;
+            if constexpr (FP8) {
+                const v4i lo = *(const v4i*)(kt + (L.k_addr ^ ((4 * c) << 4)));
+                const v4i hi = *(const v4i*)(kt + (L.k_addr ^ ((4 * c + 1) << 4)));
+                const v8i aop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                s[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, qop[c], s[t], 0, 0, 0, 0, 0, 0);
+            } else {
+                const v4i x = *(const v4i*)(kt + (L.k_addr ^ ((2 * c) << 4)));
+                s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, x), qop[c], s[t], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- mask, online softmax (lazy rescale) ----------------------------
+    // (CAUSAL: only tiles that cross some row's limit, a wave-uniform test)
+    if (CAUSAL ? __builtin_amdgcn_ballot_w64(valid < kKeyTile) != 0 : valid < kKeyTile) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (key_of_acc<FP8>(t, r, h) >= valid) s[t][r] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+    const float mxs = halves_max(mx) * cscale;
+    if (__builtin_amdgcn_ballot_w64(mxs > st.m + S::RESCALE_LOG2) != 0) {
+        const float m_new = fmaxf(st.m, mxs);
+        const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+        st.l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) st.o[dt] *= alpha;
+        st.m = m_new;
+    }
+    float psum = 0.f;
+    const float shift = (FP8 ? kPBiasLog2 : 0.f) - st.m;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], cscale, shift));
+            s[t][r] = p;
+            psum += p;
+        }
+    st.l += psum;
+
+    // ---- O^T += V^T . P^T -----------------------------------------------
+    if constexpr (FP8) {
+        v8i pop;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                // The first convert's untouched high half is overwritten by
+                // the second, so any register serves as its "old" operand.
+                int pk = __builtin_amdgcn_cvt_pk_fp8_f32(s[t][4 * q4], s[t][4 * q4 + 1],
+                                                         __float_as_int(s[t][4 * q4]), false);
+                pk = __builtin_amdgcn_cvt_pk_fp8_f32(s[t][4 * q4 + 2], s[t][4 * q4 + 3], pk, true);
+                pop[4 * t + q4] = pk;
+            }
+        // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1): keys
+        // 32*(grp>>1) + [0, 32) of column d, 8 per transposing read; the
+        // d tiles are read two at a time, one pair ahead of the MFMAs.
+        constexpr int PAIRS = DT / 2;
+        v2i x[2][8];
+        auto issue = [&](v2i (&buf)[8], int pair) {
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t addr = L.v_addr[0] ^ ((2 * (2 * pair + k)) << 4);
+                // keys 32g + 8s + m live in LDS rows (8g + m) + {0, 32, 16, 48}[s]
+                buf[4 * k + 0] = ds_read_tr8_b64<VBASE + 0 * ROW>(addr);
+                buf[4 * k + 1] = ds_read_tr8_b64<VBASE + 32 * ROW>(addr);
+                buf[4 * k + 2] = ds_read_tr8_b64<VBASE + 16 * ROW>(addr);
+                buf[4 * k + 3] = ds_read_tr8_b64<VBASE + 48 * ROW>(addr);
+            }
+        };
+        issue(x[0], 0);
+#pragma unroll
+        for (int pair = 0; pair < PAIRS; ++pair) {
+            v2i(&cur)[8] = x[pair & 1];
+            lds_results_ready(cur);
+            if (pair + 1 < PAIRS) issue(x[(pair + 1) & 1], pair + 1);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const v8i aop = {cur[4 * k][0],     cur[4 * k][1],     cur[4 * k + 1][0], cur[4 * k + 1][1],
+                                 cur[4 * k + 2][0], cur[4 * k + 2][1], cur[4 * k + 3][0], cur[4 * k + 3][1]};
+                st.o[2 * pair + k] =
+                    __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, pop, st.o[2 * pair + k], 0, 0, 0, 0, 0, 0);
+            }
+        }
+    } else {
+        v8bf pop[2][2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int e2 = 0; e2 < 8; ++e2) pop[t][u][e2] = (__bf16)s[t][8 * u + e2];
+        // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1): for score
+        // tile t and half u, keys 32t + 16u + 8*(grp>>1) + [0, 8) of column
+        // d, 4 per transposing read.
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const uint32_t a0 = L.v_addr[0] ^ ((4 * dt) << 4);
+            const uint32_t a1 = L.v_addr[1] ^ ((4 * dt) << 4);
+            v2i x[4];
+            x[0] = ds_read_tr16_b64<VBASE>(a0);
+            x[1] = ds_read_tr16_b64<VBASE>(a1);
+            x[2] = ds_read_tr16_b64<VBASE + 16 * ROW>(a0);
+            x[3] = ds_read_tr16_b64<VBASE + 16 * ROW>(a1);
+            lds_results_ready(x);
+            const v4i aop0 = {x[0][0], x[0][1], x[1][0], x[1][1]};
+            const v4i aop1 = {x[2][0], x[2][1], x[3][0], x[3][1]};
+            st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop0), pop[0][0], st.o[dt], 0, 0, 0);
+            st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop1), pop[0][1], st.o[dt], 0, 0, 0);
+            v2i y[4];
+            y[0] = ds_read_tr16_b64<VBASE + 32 * ROW>(a0);
+            y[1] = ds_read_tr16_b64<VBASE + 32 * ROW>(a1);
+            y[2] = ds_read_tr16_b64<VBASE + 48 * ROW>(a0);
+            y[3] = ds_read_tr16_b64<VBASE + 48 * ROW>(a1);
+            lds_results_ready(y);
+            const v4i aop2 = {y[0][0], y[0][1], y[1][0], y[1][1]};
+            const v4i aop3 = {y[2][0], y[2][1], y[3][0], y[3][1]};
+            st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop2), pop[1][0], st.o[dt], 0, 0, 0);
+            st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop3), pop[1][1], st.o[dt], 0, 0, 0);
+        }
+    }
+}
+
+// Wait for tile `cur` (in BUF), start the prefetch of `nxt` into the other
+// buffer, then compute `cur`.
+template <class S, int BUF, bool CAUSAL>
+__device__ __forceinline__ void tile_step(const FwdArgs& a, const TileCursor& cur, const TileCursor& nxt,
+                                          uint8_t* lds, int wave, int tid, int h, const LaneMap<S>& L,
+                                          const QOperand<S> (&qop)[S::QK], float cscale, SoftmaxState<S>& st,
+                                          int row_limit) {
+    const int valid = min(kKeyTile, cur.n - cur.base);
+    uint8_t* const lds_v = lds + BUF * 2 * S::TILE + S::TILE;
+    if constexpr (S::NBUF == 2) {
+        wait_vmem();      // this wave's loads of the current tile have landed
+        __syncthreads();  // ... and every wave's; the other buffer is free
+        if (nxt.e < a.num_entries) stage_tile_async<S, BUF ^ 1>(a, nxt, lds, wave, L);
+        if (valid < kKeyTile) {
+            zero_masked_v<S>(lds_v, valid, tid);
+            __syncthreads();
+        }
+    } else {
+        __syncthreads();  // previous tile fully consumed
+        if constexpr (S::WIDEN) {
+            stage_tile_sync<S>(a, cur, valid, lds, tid);
+        } else {
+            stage_tile_async<S, 0>(a, cur, lds, wave, L);
+            wait_vmem();
+            __syncthreads();
+            if (valid < kKeyTile) zero_masked_v<S>(lds_v, valid, tid);
+        }
+        __syncthreads();
+    }
+    compute_tile<S, BUF, CAUSAL>(lds, CAUSAL ? min(valid, row_limit - cur.base) : valid, qop, cscale, L, h, st);
+}
+
+// CAUSAL: causal attention of the current tokens among themselves (their
+// K/V are one page of block_size tokens in global order, no block table):
+// row (rank, token) sees current keys up to its own global position.  The
+// epilogue can then merge the result with a history output (merge_o,
+// merge_lse) by log-sum-exp.
+template <int D, bool STORE8, bool FP8, bool CAUSAL = false>
+__global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_fwd_kernel(FwdArgs a) {
+    using S = TileShape<D, STORE8, FP8>;
+    constexpr int ROW = S::ROW, CHUNKS = S::CHUNKS, QK = S::QK, DT = S::DT;
+
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S::NBUF * 2 * S::TILE];
+    __shared__ int wave_limit[kWaves];
+
+    // ---- XCD-aware work mapping ------------------------------------------
+    // Workgroups are dealt to the 8 XCDs round-robin by launch index; give
+    // each XCD a contiguous range of (KV head, row tile) work items so that
+    // the workgroups sharing an XCD's L2 stream the same KV head together.
+    // CAUSAL: work grows with the row tile (later ranks see more current
+    // keys) and the keys fit in L2 anyway, so launch the heaviest tiles
+    // first, both heads alike, and let the early finishers take the light
+    // ones (longest-first balancing over all XCDs).
+    const int items = a.row_tiles * a.num_kv_heads;
+    int head, row_tile;
+    if constexpr (CAUSAL) {
+        const int item = blockIdx.x;
+        if (item >= items) return;
+        head = item % a.num_kv_heads;
+        row_tile = a.row_tiles - 1 - item / a.num_kv_heads;
+    } else {
+        const int per_xcd = (items + 7) / 8;
+        const int item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+        if (item >= items) return;
+        head = item / a.row_tiles;
+        row_tile = item - head * a.row_tiles;
+    }
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 31;  // query column of the score tile / A-operand row
+    const int h = lane >> 5;  // k-group (lane half)
+    const int grp = lane >> 4;
+    const int gl = lane & 15;
+
+    // ---- this lane's query row -------------------------------------------
+    const int row = row_tile * kRowsPerGroup + wave * kRowsPerWave + j;
+    const bool row_ok = row < a.rows_per_head;
+    const int rowc = row_ok ? row : a.rows_per_head - 1;
+    const int rank = rowc / a.group_rows;
+    const int rem = rowc - rank * a.group_rows;
+    const int head_in_group = rem / a.local_q;
+    const int tok = rem - head_in_group * a.local_q;
+    const int64_t row_off =
+        ((int64_t)(rank * a.num_q_heads + head * a.group + head_in_group) * a.local_q + tok) * D * 2;
+    const uint8_t* const qrow = a.q + row_off;
+
+    // ---- Q^T operand (register resident for the whole history) ------------
+    QOperand<S> qop[QK];
+    float cscale;
+    if constexpr (FP8) {
+        // lane (j, h) holds d = 64c + 32h + [0, 32) of its row, as e4m3.
+        float amax = 0.f;
+#pragma unroll
+        for (int c = 0; c < QK; ++c) {
+#pragma unroll
+            for (int part = 0; part < 4; ++part) {
+                const v4i raw = *(const v4i*)(qrow + (64 * c + 32 * h) * 2 + 16 * part);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const uint32_t u = (uint32_t)raw[w];
+                    amax = fmaxf(amax, fabsf(bf16_bits_to_f32(u & 0xffffu)));
+                    amax = fmaxf(amax, fabsf(bf16_bits_to_f32(u >> 16)));
+                }
+            }
+        }
+        amax = halves_max(amax);
+        const float inv = amax > 0.f ? kFp8Max / amax : 1.f;
+        const float sigma = amax > 0.f ? amax / kFp8Max : 1.f;
+#pragma unroll
+        for (int c = 0; c < QK; ++c) {
+#pragma unroll
+            for (int part = 0; part < 4; ++part) {
+                const v4i raw = *(const v4i*)(qrow + (64 * c + 32 * h) * 2 + 16 * part);
+#pragma unroll
+                for (int w = 0; w < 2; ++w) {
+                    const uint32_t u0 = (uint32_t)raw[2 * w], u1 = (uint32_t)raw[2 * w + 1];
+                    int pk = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_bits_to_f32(u0 & 0xffffu) * inv,
+                                                             bf16_bits_to_f32(u0 >> 16) * inv, 0, false);
+                    pk = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_bits_to_f32(u1 & 0xffffu) * inv,
+                                                         bf16_bits_to_f32(u1 >> 16) * inv, pk, true);
+                    qop[c][2 * part + w] = pk;
+                }
+            }
+        }
+        cscale = sigma * a.score_scale;
+    } else {
+        // lane (j, h) holds d = 16c + 8h + [0, 8) of its row.
+#pragma unroll
+        for (int c = 0; c < QK; ++c) {
+            const v4i raw = *(const v4i*)(qrow + (16 * c + 8 * h) * 2);
+            qop[c] = __builtin_bit_cast(v8bf, raw);
+        }
+        cscale = a.score_scale;
+    }
+
+    // ---- per-lane LDS / DMA offsets ---------------------------------------
+    // Row offsets are multiples of ROW (a power of two) and the chunk field
+    // lies below ROW, so XOR-ing a constant into the chunk field is one v_xor.
+    LaneMap<S> L;
+    {
+        const int row = lds_row<FP8>(key_of_row<FP8>(0, j));
+        const int first_chunk = FP8 ? 2 * h : h;
+        L.k_addr = row * ROW + ((first_chunk ^ chunk_swizzle<FP8, CHUNKS>(row)) << 4);
+    }
+    if constexpr (FP8) {
+        // key 32*(grp>>1) + (gl>>1) (+ 8s for the other reads) -> row below
+        const int row = lds_row<FP8>(32 * (grp >> 1) + (gl >> 1));
+        L.v_addr[0] = row * ROW + (((grp & 1) ^ chunk_swizzle_v<FP8, CHUNKS>(row)) << 4) + 8 * (gl & 1);
+    } else {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const int vkey = 8 * (grp >> 1) + 4 * s2 + (gl >> 2);  // + 16u + 32t: same swizzle
+            const int dbyte = 2 * (16 * (grp & 1) + 4 * (gl & 3));
+            L.v_addr[s2] = vkey * ROW + (((dbyte >> 4) ^ chunk_swizzle<FP8, CHUNKS>(vkey)) << 4) + (dbyte & 15);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < (S::DMA_SPLIT ? S::DMA_PER_WAVE : 1); ++i) {
+        const int byte = (4 * i + wave) * 1024 + lane * 16;
+        const int row = byte / ROW;
+        const int pos = (byte % ROW) / 16;
+        L.dma_off[i] = lds_row<FP8>(row) * S::GROW + (pos ^ chunk_swizzle<FP8, CHUNKS>(row)) * 16;
+        L.dma_off_v[i] = lds_row<FP8>(row) * S::GROW + (pos ^ chunk_swizzle_v<FP8, CHUNKS>(row)) * 16;
+    }
+
+    // ---- walk the block table -----------------------------------------------
+    SoftmaxState<S> st;
+    st.m = -INFINITY;
+    st.l = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) st.o[dt] = v16f{};
+
+    // CAUSAL: the row sees current keys [0, g] (g its global current
+    // position, layout.py:10-16 inverted); the workgroup stops after the
+    // tile holding the largest g of its rows.
+    int row_limit = 0, group_limit = 0;
+    if constexpr (CAUSAL) {
+        row_limit = ((tok / a.interleave) * a.pcp + rank) * a.interleave + tok % a.interleave + 1;
+        int w = row_limit;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) w = max(w, __shfl_xor(w, off));
+        if (lane == 0) wave_limit[wave] = w;
+        __syncthreads();
+        group_limit = wave_limit[0];
+#pragma unroll
+        for (int i = 1; i < kWaves; ++i) group_limit = max(group_limit, wave_limit[i]);
+    }
+    auto advance = [&](const TileCursor& c) {
+        if constexpr (CAUSAL) {
+            const TileCursor n = next_current_tile(a, head, c);
+            return n.base < group_limit ? n : TileCursor{a.num_entries, 0, 0, 0};
+        } else {
+            return next_tile(a, head, c);
+        }
+    };
+
+    TileCursor cur = advance(TileCursor{-1, 0, 0, 0});
+    if constexpr (S::NBUF == 2) {
+        if (cur.e < a.num_entries) stage_tile_async<S, 0>(a, cur, lds, wave, L);
+    }
+    while (cur.e < a.num_entries) {
+        TileCursor nxt = advance(cur);
+        tile_step<S, 0, CAUSAL>(a, cur, nxt, lds, wave, tid, h, L, qop, cscale, st, row_limit);
+        cur = nxt;
+        if constexpr (S::NBUF == 2) {
+            if (cur.e >= a.num_entries) break;
+            nxt = advance(cur);
+            tile_step<S, 1, CAUSAL>(a, cur, nxt, lds, wave, tid, h, L, qop, cscale, st, row_limit);
+            cur = nxt;
+        }
+    }
+
+    // ---- epilogue: O = O^T / l, bf16; log-sum-exp; merge -------------------
+    const float l_tot = halves_sum(st.l);
+    float scale = l_tot > 0.f ? a.v_scale / l_tot : 0.f;
+    // sum_k exp(score_k) = l * 2^(m - bias): P was 2^(x - m + bias)
+    float lse = l_tot > 0.f ? __logf(l_tot) + (st.m - (FP8 ? kPBiasLog2 : 0.f)) * kLn2 : -INFINITY;
+    const int64_t row_index = row_off / (D * 2);
+    float hist_weight = 0.f;
+    if (CAUSAL && a.merge_o) {
+        // out = (e^lse_h O_h + e^lse O) / (e^lse_h + e^lse)
+        const float lse_h = a.merge_lse[row_index];
+        const float mx = fmaxf(lse_h, lse);
+        const float wh = lse_h == -INFINITY ? 0.f : __expf(lse_h - mx);
+        const float wc = __expf(lse - mx);
+        hist_weight = wh / (wh + wc);
+        scale *= wc / (wh + wc);
+        lse = mx + __logf(wh + wc);
+    }
+    if (row_ok) {
+        uint8_t* const orow = a.out + row_off;
+        const uint8_t* const hrow = CAUSAL && a.merge_o ? a.merge_o + row_off : nullptr;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int d = 32 * dt + 8 * r4 + 4 * h;
+                float o0 = st.o[dt][4 * r4 + 0] * scale, o1 = st.o[dt][4 * r4 + 1] * scale;
+                float o2 = st.o[dt][4 * r4 + 2] * scale, o3 = st.o[dt][4 * r4 + 3] * scale;
+                if (CAUSAL && hrow) {
+                    const v2i hv = *(const v2i*)(hrow + 2 * d);
+                    o0 = fmaf(hist_weight, bf16_bits_to_f32((uint32_t)hv[0] & 0xffffu), o0);
+                    o1 = fmaf(hist_weight, bf16_bits_to_f32((uint32_t)hv[0] >> 16), o1);
+                    o2 = fmaf(hist_weight, bf16_bits_to_f32((uint32_t)hv[1] & 0xffffu), o2);
+                    o3 = fmaf(hist_weight, bf16_bits_to_f32((uint32_t)hv[1] >> 16), o3);
+                }
+                const __bf16 v0 = (__bf16)o0, v1 = (__bf16)o1, v2 = (__bf16)o2, v3 = (__bf16)o3;
+                const uint32_t w0 = (uint32_t)__builtin_bit_cast(uint16_t, v0) |
+                                    ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16);
+                const uint32_t w1 = (uint32_t)__builtin_bit_cast(uint16_t, v2) |
+                                    ((uint32_t)__builtin_bit_cast(uint16_t, v3) << 16);
+                *(v2i*)(orow + 2 * d) = v2i{(int)w0, (int)w1};
+            }
+        if (a.lse && h == 0) a.lse[row_index] = lse;
+    }
+}
+
+}  // namespace pcpa
