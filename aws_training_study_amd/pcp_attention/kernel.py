@@ -66,7 +66,9 @@ class HistoryAttentionKernel:
     page_valid_len=None, k_scale=1.0, v_scale=1.0, out=None) -> out``
 
     * ``q``: ``[pcp, Hq, local_q, D]`` bfloat16 on the GPU (every rank's Q
-      shard, ``layout.stacked_query``).
+      shard, ``layout.stacked_query``), or the reference's per-rank list of
+      ``[Hq, local_q, D]`` shards (stacked here).  ``out[r]`` is rank r's
+      output; ``list(out)`` gives the per-rank list.
     * ``kv_pages``: ``[num_pages, 2 * Hkv * block_size * D]`` in the config's
       ``kv_dtype``; row ``p`` is a ``pack_local_kv`` row.
     * ``block_table``: int ``[pcp, max_local_blocks]`` page of each cache block.
@@ -169,6 +171,11 @@ class HistoryAttentionKernel:
             raise ValueError(f"precision must be one of {PRECISIONS}, got {precision!r}")
         if exp2 not in EXP2_MODES:
             raise ValueError(f"exp2 must be one of {EXP2_MODES}, got {exp2!r}")
+        if isinstance(q, (list, tuple)):
+            # the reference's per-rank form: one [Hq, local_q, D] shard per rank
+            if len(q) != cfg.pcp_size:
+                raise ValueError(f"expected {cfg.pcp_size} per-rank Q shards, got {len(q)}")
+            q = torch.stack(list(q))
         if not q.is_cuda:
             raise ValueError("q must be a GPU tensor")
         device = q.device

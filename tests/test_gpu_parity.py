@@ -230,3 +230,17 @@ def test_fp8_exp2_modes(exp2, actual, cuda_device):
     diff = np.abs(out - other.float().cpu().numpy())
     print(f"fast vs exact exp2: max_abs={diff.max():.3e} mean_abs={diff.mean():.3e}", flush=True)
     assert diff.max() <= MAX_ABS_TOL and diff.mean() <= MEAN_ABS_TOL
+
+
+def test_per_rank_list_input(cuda_device):
+    """The reference's per-rank Q list gives the stacked call's output, rank by rank."""
+    problem = build_workload_problem("tiny-gqa4-d64-bf16", seed=9)
+    gpu = problem.to(cuda_device)
+    kernel = make_history_attention_kernel(problem.config)
+    stacked = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len)
+    shards = [gpu.q_stacked[r] for r in range(problem.config.pcp_size)]
+    listed = kernel(shards, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len)
+    torch.cuda.synchronize()
+    assert torch.equal(listed, stacked)
+    with pytest.raises(ValueError, match="per-rank Q shards"):
+        kernel(shards[:-1], gpu.kv_pages, gpu.block_table)
