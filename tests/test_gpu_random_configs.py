@@ -1,0 +1,89 @@
+"""Seeded random configurations through every kernel variant, against the
+float64 oracle on every output row.
+
+Each case draws pcp size, interleave, block size, heads, head dim, cache
+dtype, MFMA precision and a runtime history length (generally not aligned to
+anything) from a fixed seed, so the set is the same on every run.  Bar:
+max-abs <= 2e-2 and mean-abs <= 2e-3, except that e4m3 MFMAs over short
+histories (where the e4m3 rounding of Q and P is not averaged away) are
+held to the one-pass kernel's own error plus 4e-3 when the bar is missed.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from aws_training_study_amd.pcp_attention import make_history_attention_kernel
+from aws_training_study_amd.pcp_attention.config import PCPAttentionConfig
+from aws_training_study_amd.pcp_attention.workloads import build_paged_problem
+from oracle import pcp_oracle as orc
+
+from test_gpu_parity import MAX_ABS_TOL, MEAN_ABS_TOL, _real_history
+
+pytestmark = pytest.mark.gpu
+
+CASES = 16
+
+
+def _draw(i: int) -> tuple[PCPAttentionConfig, str, dict]:
+    rng = np.random.default_rng(1000 + i)
+    for _ in range(100):
+        pcp = int(rng.choice([1, 2, 3, 4, 8]))
+        il = int(rng.choice([16, 32, 64]))
+        blk = int(rng.choice([64, 128, 256, 512]))
+        if blk % il:
+            continue
+        d = int(rng.choice([64, 128, 256, 256]))
+        hkv = int(rng.choice([1, 2, 4]))
+        group = int(rng.choice([1, 2, 4, 8]))
+        stride = pcp * il
+        q_len = stride * int(rng.integers(1, max(2, 256 // stride) + 1))
+        max_hist = stride * int(rng.integers(1, max(2, 8192 // stride) + 1))
+        actual = int(rng.integers(1, max_hist + 1))
+        kv_dtype = str(rng.choice(["fp8_e4m3fn", "fp8_e4m3fn", "bfloat16"]))
+        try:
+            cfg = PCPAttentionConfig(pcp_size=pcp, current_len=q_len, max_history_len=max_hist,
+                                     actual_history_len=actual, block_size=blk, interleave_size=il,
+                                     num_q_heads=hkv * group, num_kv_heads=hkv, head_dim=d, kv_dtype=kv_dtype,
+                                     backend="hip").validate()
+        except ValueError:
+            continue
+        precision = str(rng.choice(["fp8", "fp8", "bf16"])) if kv_dtype == "fp8_e4m3fn" else "auto"
+        kw = {"precision": precision}
+        if precision == "fp8" and d == 256:
+            kw["exp2"] = str(rng.choice(["fast", "exact"]))
+            kw["splits"] = int(rng.choice([1, 1, 2, 3]))
+        return cfg, kv_dtype, kw
+    raise AssertionError("no valid configuration drawn")
+
+
+@pytest.mark.parametrize("i", range(CASES))
+def test_random_configuration(i, cuda_device):
+    cfg, kv_dtype, kw = _draw(i)
+    print(f"case {i}: pcp={cfg.pcp_size} il={cfg.interleave_size} blk={cfg.block_size} Hq/Hkv={cfg.num_q_heads}/"
+          f"{cfg.num_kv_heads} D={cfg.head_dim} Q={cfg.current_len} hist={cfg.actual_history_len}/"
+          f"{cfg.max_history_len} {kv_dtype} {kw}", flush=True)
+    problem = build_paged_problem(cfg, seed=2000 + i, kv_scale="per_tensor" if kv_dtype != "bfloat16" else "none")
+    gpu = problem.to(cuda_device)
+    kernel = make_history_attention_kernel(cfg)
+    out = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len,
+                 k_scale=problem.k_scale, v_scale=problem.v_scale, **kw)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    q, k, v = _real_history(problem)
+    exp = orc.expected_stacked(q, k, v, orc.OracleShape.from_config(cfg))
+    max_abs, mean_abs = orc.max_abs_and_mean_abs(got, exp)
+    print(f"  max_abs={max_abs:.3e} mean_abs={mean_abs:.3e}", flush=True)
+    if max_abs <= MAX_ABS_TOL and mean_abs <= MEAN_ABS_TOL:
+        return
+    assert kw.get("precision") == "fp8", "BF16 MFMA path outside the bar"
+    one = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len,
+                 k_scale=problem.k_scale, v_scale=problem.v_scale, precision="fp8", splits=1)
+    torch.cuda.synchronize()
+    one_max, one_mean = orc.max_abs_and_mean_abs(one.float().cpu().numpy(), exp)
+    print(f"  short-history e4m3 case: one-pass max_abs={one_max:.3e} mean_abs={one_mean:.3e}", flush=True)
+    assert cfg.actual_history_len < 2048, "e4m3 path outside the bar on a long history"
+    assert max_abs <= one_max + 4e-3 and mean_abs <= max(MEAN_ABS_TOL, one_mean + 1e-3)
