@@ -12,7 +12,8 @@ pinned (tests/test_oracle.py):
 * index maps (owner/local position, positions per rank, shard/gather, pack,
   block mask) - the reference tests' known answers (tests/test_layout.py,
   test_kernel_pack.py, test_runner.py), the README closed form checked by
-  brute-force enumeration, and hand-written tables in tests/golden.
+  brute-force enumeration, and the hand-worked table in
+  tests/golden/owner_pcp3_il2.json.
 * dense attention - float64; checked against a per-row brute-force loop, a
   closed form (identical keys give the mean of V) and one-hot limits.
 * ring model - equals dense attention (tests/test_reference.py:8-56 in the
