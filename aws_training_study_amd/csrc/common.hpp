@@ -112,7 +112,7 @@ __device__ __forceinline__ int key_of_row(int t, int rho) {
 // row bits, and the per-lane part of every K, V and DMA address is the same
 // for all tiles t, reads s and DMA blocks.  BF16 tiles keep key order.
 template <bool FP8>
-__device__ __forceinline__ int lds_row(int key) {
+__host__ __device__ __forceinline__ constexpr int lds_row(int key) {
     if constexpr (FP8) return (key & ~0x28) | ((key >> 2) & 0x8) | ((key << 2) & 0x20);
     return key;
 }

@@ -125,18 +125,40 @@ struct Shape {
     static constexpr int QK = D / 64;        // k-steps of the score MFMA
     static constexpr int NX = 2 * QK;        // score MFMAs per tile
     static constexpr int DT = D / 32;        // PV MFMAs per tile
-    static constexpr int DPW = TILE / 1024 / kWaves;  // 1 KB DMA blocks per wave per K (or V) tile
-    // DMA block 8i + wave lands 32i LDS rows after block `wave` (rows
-    // < 32): lds_row maps row bit 5 to key bit 3, so its chunk is 8i keys
-    // further on, with the same swizzle.
-    static constexpr int DMA_KEY_STEP = 8;
-    static_assert(DPW == 1 || 8 * 1024 / ROW == 32, "block rows must step by 32");
     // Softmax micro-slices [pv_begin(i), pv_begin(i+1)) run beside PV MFMA i.
     static constexpr int pv_begin(int i) {
         constexpr int b256[] = {0, 4, 6, 7, 8, 9, 10, 11, 14};
         constexpr int b128[] = {0, 5, 8, 11, 14};
         return D == 256 ? b256[i] : b128[i];
     }
+};
+
+// Who moves the K and V tiles: the last WAVES waves of the workgroup issue
+// the LDS-DMA of every K and V tile and each waits for its own blocks; the
+// barrier after the waits publishes them to all waves.  WAVES = kWaves / 2
+// is the group that runs PV first (one wave per SIMD); with it the plain
+// launches measured about 1% faster than with all eight waves issuing, but
+// the log-sum-exp and split instantiations then spill Q fragments inside
+// the loop, so those keep WAVES = kWaves.
+template <int D, int WAVES>
+struct DmaPlan {
+    static_assert(WAVES == kWaves || WAVES == kWaves / 2, "DMA from all waves or from the late group");
+    static constexpr int ROW = D;
+    static constexpr int DPW = kKeyTile * ROW / 1024 / WAVES;  // 1 KB blocks per wave per K (or V) tile
+    static constexpr int STRIDE = WAVES * 1024;                // LDS bytes between a wave's blocks
+    // A wave's block i lands i * BLOCK_ROWS LDS rows after its block 0
+    // (rows < BLOCK_ROWS).  lds_row permutes row bits, so block i holds the
+    // keys lds_row(i * BLOCK_ROWS) further on; a multiple of 16 rows keeps
+    // the chunk swizzle of block 0.
+    static constexpr int BLOCK_ROWS = STRIDE / ROW;
+    static_assert(BLOCK_ROWS % 16 == 0, "DMA blocks must share the chunk swizzle");
+    // Byte offset of block i's keys; addressed from the middle of their span
+    // (MID) they fit the load's 13-bit signed immediate offset.
+    static constexpr int offset(int i) { return lds_row<true>(i * BLOCK_ROWS) * ROW; }
+    static constexpr int MID = offset(DPW - 1) / 2;
+    static_assert(MID < 4096, "DMA block offsets must fit the immediate");
+    __device__ static bool issues(int wave) { return wave >= kWaves - WAVES; }
+    __device__ static int block(int wave) { return wave - (kWaves - WAVES); }
 };
 
 struct Lanes {
@@ -235,53 +257,58 @@ __device__ __forceinline__ void softmax_slices(const v16f (&s)[2], v8i& p, Softm
     }
 }
 
-// Key of the lane's chunk of DMA block i (LDS byte (8i + wave) * 1024 +
-// 16 * lane, rows permuted by lds_row).
-template <class S>
+// Key of the lane's chunk of DMA block i (LDS byte i * P::STRIDE +
+// wave_off + 16 * lane, rows permuted by lds_row).
+template <class P>
 __device__ __forceinline__ int dma_chunk_key(int i, int wave_off) {
-    return lds_row<true>((i * kWaves * 1024 + wave_off + __lane_id() * 16) / S::ROW);
+    return lds_row<true>((i * P::STRIDE + wave_off + __lane_id() * 16) / P::ROW);
+}
+
+// DMA blocks I.. of a full tile into dst.  mid is the lane's source address
+// of block 0 plus P::MID: the blocks' offsets from it are immediates of the
+// loads rather than 64-bit constants held in registers.  The immediate is
+// added to the LDS address as well, so the LDS operand is taken that much
+// lower (it stays non-negative: imm <= MID < STRIDE <= I * STRIDE for I > 0).
+template <class P, int I = 0>
+__device__ __forceinline__ void dma_blocks(const uint8_t* mid, uint8_t* dst) {
+    if constexpr (I < P::DPW) {
+        constexpr int imm = P::offset(I) - P::MID;
+        static_assert(I == 0 || imm < I * P::STRIDE, "LDS operand must stay inside the block");
+        uint8_t* const d = dst + (I * P::STRIDE - imm);
+        __builtin_amdgcn_global_load_lds(mid, PCPA_LDS(void, d), 16, imm, 0);
+        dma_blocks<P, I + 1>(mid, dst);
+    }
 }
 
 // Issue the K tile of cursor c into K stage st.  (Pointers are formed in
 // plain variables: address-space casts of expressions that depend on S trip
 // the host compilation pass.)
-template <class S>
+template <class S, class P>
 __device__ __forceinline__ void load_k(const FwdArgs& a, const TileCursor& c, uint8_t* lds, int st, int wave_off,
                                        uint32_t off) {
-    const uint8_t* const kt = a.kv + c.k_off + (int64_t)c.base * S::ROW + off;
-    uint8_t* const dst = lds + st * S::TILE + wave_off;
-#pragma unroll
-    for (int i = 0; i < S::DPW; ++i) {
-        const uint8_t* const src = kt + i * S::DMA_KEY_STEP * S::ROW;
-        uint8_t* const d = dst + i * (kWaves * 1024);
-        __builtin_amdgcn_global_load_lds(src, PCPA_LDS(void, d), 16, 0, 0);
-    }
+    const uint8_t* const kt = a.kv + c.k_off + (int64_t)c.base * S::ROW + off + P::MID;
+    dma_blocks<P>(kt, lds + st * S::TILE + wave_off);
 }
 
 // Issue the V tile of cursor c into V stage st.  Rows past the valid length
 // (all rows of a phantom tile) come from zero_chunk, so V stages of masked
 // keys hold zeros and the number of loads per tile never changes.
-template <class S>
+template <class S, class P>
 __device__ __forceinline__ void load_v(const FwdArgs& a, const TileCursor& c, uint8_t* lds, int st, int wave_off,
                                        uint32_t off, bool real) {
     const uint8_t* const vt =
-        a.kv + c.k_off + (int64_t)c.base * S::ROW + (int64_t)a.num_kv_heads * a.head_stride + off;
+        a.kv + c.k_off + (int64_t)c.base * S::ROW + (int64_t)a.num_kv_heads * a.head_stride + off + P::MID;
     uint8_t* const dst = lds + S::RING + st * S::TILE + wave_off;
     const int valid = real ? c.n - c.base : 0;
     if (valid >= kKeyTile) {
-#pragma unroll
-        for (int i = 0; i < S::DPW; ++i) {
-            const uint8_t* const src = vt + i * S::DMA_KEY_STEP * S::ROW;
-            uint8_t* const d = dst + i * (kWaves * 1024);
-            __builtin_amdgcn_global_load_lds(src, PCPA_LDS(void, d), 16, 0, 0);
-        }
+        dma_blocks<P>(vt, dst);
     } else {
         const uint8_t* const zero = zero_chunk;
 #pragma unroll
-        for (int i = 0; i < S::DPW; ++i) {
+        for (int i = 0; i < P::DPW; ++i) {
             const uint8_t* const src =
-                dma_chunk_key<S>(i, wave_off) < valid ? vt + i * S::DMA_KEY_STEP * S::ROW : zero;
-            uint8_t* const d = dst + i * (kWaves * 1024);
+                dma_chunk_key<P>(i, wave_off) < valid ? vt + (P::offset(i) - P::MID) : zero;
+            uint8_t* const d = dst + i * P::STRIDE;
             __builtin_amdgcn_global_load_lds(src, PCPA_LDS(void, d), 16, 0, 0);
         }
     }
@@ -381,7 +408,7 @@ __device__ __forceinline__ void pv_half(uint32_t v_addr, v2i (&xv0)[4], v16f (&o
 }
 
 // Iteration j, J4 = j mod 4; LATE: waves 4-7 (PV half first, one tile behind).
-template <int D, int J4, bool LATE, bool FAST>
+template <int D, int J4, bool LATE, bool FAST, int DMAW>
 __device__ __forceinline__ void iteration(const FwdArgs& a, uint8_t* lds, int wave, int h, const Lanes& L,
                                           const v8i (&q)[Shape<D>::QK], v16f (&s)[2], v8i (&pbuf)[2],
                                           v16f (&o)[Shape<D>::DT], SoftmaxRow& sm, Cursors& cs, int head) {
@@ -390,21 +417,28 @@ __device__ __forceinline__ void iteration(const FwdArgs& a, uint8_t* lds, int wa
 
     // ---- K(j) and V(j-1) have landed (for every wave) ----------------------
     // Loads issued one iteration ago may be pending: V(j), and K(j+1) if tile
-    // j+1 is real.
-    if (is_real(a, cs.c1))
-        wait_vmem_le<2 * S::DPW>();
-    else
-        wait_vmem_le<S::DPW>();
+    // j+1 is real.  Each wave that issues DMA waits for its own blocks; the
+    // barrier then publishes all of them.
+    using P = DmaPlan<D, DMAW>;
+    constexpr bool dma = DMAW == kWaves || LATE;
+    if constexpr (dma) {
+        if (is_real(a, cs.c1))
+            wait_vmem_le<2 * P::DPW>();
+        else
+            wait_vmem_le<P::DPW>();
+    }
     __builtin_amdgcn_s_barrier();
     // K stage (j+2) % 4 held K(j-2) and V stage (j+1) % 4 held V(j-3); both
     // were last read in iteration j-1.  The wave offset and operand bases
     // are made opaque so that the DMA destinations and operand addresses are
     // recomputed in the loop rather than hoisted and spilled.
-    int wave_off = wave * 1024;
+    int wave_off = P::block(wave) * 1024;
     uint32_t k_addr = L.k_addr, v_addr = L.v_addr;
     asm volatile("" : "+s"(wave_off), "+v"(k_addr), "+v"(v_addr));
-    if (is_real(a, cs.c2)) load_k<S>(a, cs.c2, lds, (J4 + 2) % kStages, wave_off, L.dma_k);
-    load_v<S>(a, cs.c1, lds, (J4 + 1) % kStages, wave_off, L.dma_v, is_real(a, cs.c1));
+    if constexpr (dma) {
+        if (is_real(a, cs.c2)) load_k<S, P>(a, cs.c2, lds, (J4 + 2) % kStages, wave_off, L.dma_k);
+        load_v<S, P>(a, cs.c1, lds, (J4 + 1) % kStages, wave_off, L.dma_v, is_real(a, cs.c1));
+    }
 
     v2i xv[4];
     if constexpr (!LATE) {
@@ -428,23 +462,23 @@ __device__ __forceinline__ void iteration(const FwdArgs& a, uint8_t* lds, int wa
 }
 
 // The loop of one wave group; iteration j runs while j <= T + 1 (T tiles).
-template <int D, bool LATE, bool FAST>
+template <int D, bool LATE, bool FAST, int DMAW>
 __device__ __forceinline__ void walk(const FwdArgs& a, uint8_t* lds, int wave, int h, const Lanes& L,
                                      const v8i (&q)[Shape<D>::QK], v16f (&s)[2], v8i (&pbuf)[2],
                                      v16f (&o)[Shape<D>::DT], SoftmaxRow& sm, Cursors cs, int head) {
     for (;;) {
         // after iteration j the loop ends if tile j-1 was past the last tile
         bool done = cs.cm1.e >= a.num_entries;
-        iteration<D, 0, LATE, FAST>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+        iteration<D, 0, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
         if (done) break;
         done = cs.cm1.e >= a.num_entries;
-        iteration<D, 1, LATE, FAST>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+        iteration<D, 1, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
         if (done) break;
         done = cs.cm1.e >= a.num_entries;
-        iteration<D, 2, LATE, FAST>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+        iteration<D, 2, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
         if (done) break;
         done = cs.cm1.e >= a.num_entries;
-        iteration<D, 3, LATE, FAST>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+        iteration<D, 3, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
         if (done) break;
     }
 }
@@ -458,6 +492,8 @@ template <int D, bool FAST, bool LSE, bool SPLIT = false>
 __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     using S = Shape<D>;
     constexpr int QK = S::QK, DT = S::DT, ROW = S::ROW, CHUNKS = S::CHUNKS;
+    constexpr int DMAW = LSE || SPLIT ? kWaves : kWaves / 2;
+    using P = DmaPlan<D, DMAW>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * S::RING];
 
     // ---- XCD-aware work mapping (as history_fwd_kernel) ---------------------
@@ -549,8 +585,8 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
         const int vrow = lds_row<true>(32 * (grp >> 1) + (gl >> 1));
         L.v_addr = base + S::RING + vrow * ROW + (((grp & 1) ^ chunk_swizzle_v<true, CHUNKS>(vrow)) << 4) +
                    8 * (gl & 1);
-        // DMA block `wave` lands at LDS byte wave * 1024 + 16 * lane.
-        const int byte = wave * 1024 + lane * 16;
+        // A DMA wave's block 0 lands at LDS byte P::block(wave) * 1024 + 16 * lane.
+        const int byte = P::block(wave) * 1024 + lane * 16;
         const int drow = byte / ROW;
         const int pos = (byte % ROW) / 16;
         const int key = lds_row<true>(drow);
@@ -578,13 +614,16 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
         cs.c1 = next_tile(a, head, first);
         cs.c2 = is_real(a, cs.c1) ? next_tile(a, head, cs.c1) : cs.c1;
         // K(0), then V(0) and K(1) as if requested at the top of iteration -1.
-        load_k<S>(a, cs.c0, lds, 0, wave * 1024, L.dma_k);
-        load_v<S>(a, cs.c0, lds, 0, wave * 1024, L.dma_v, true);
-        if (is_real(a, cs.c1)) load_k<S>(a, cs.c1, lds, 1, wave * 1024, L.dma_k);
+        if (P::issues(wave)) {
+            const int wave_off = P::block(wave) * 1024;
+            load_k<S, P>(a, cs.c0, lds, 0, wave_off, L.dma_k);
+            load_v<S, P>(a, cs.c0, lds, 0, wave_off, L.dma_v, true);
+            if (is_real(a, cs.c1)) load_k<S, P>(a, cs.c1, lds, 1, wave_off, L.dma_k);
+        }
         if (wave < kWaves / 2)
-            walk<D, false, FAST>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+            walk<D, false, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
         else
-            walk<D, true, FAST>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+            walk<D, true, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
     }
 
     // ---- epilogue: O = O^T / l, bf16; log-sum-exp ---------------------------
