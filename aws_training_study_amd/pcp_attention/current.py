@@ -131,8 +131,10 @@ class PrefillAttention:
 
     ``prefill(q, kv_pages, block_table, kv_current, *, page_valid_len=None,
     k_scale=1.0, v_scale=1.0, precision="auto", exp2="fast",
-    return_lse=False)`` - two launches on the current stream; the output
-    buffer of the first is updated in place by the second.
+    return_lse=False, workspace=None)`` - two launches on the current
+    stream; the output buffer of the first is updated in place by the
+    second (``workspace``: the history's split workspace, as for
+    ``HistoryAttentionKernel``).
     """
 
     def __init__(self, config: PCPAttentionConfig):
@@ -141,15 +143,18 @@ class PrefillAttention:
         self.config = self.history.config
 
     def graphed(self, q, kv_pages, block_table, kv_current, *, warmup: int = 1, **kwargs):
-        """Both launches captured into one HIP graph (``launch.GraphedLaunch``)."""
+        """Both launches captured into one HIP graph (``launch.GraphedLaunch``),
+        with a split workspace of the graph's own when the history is split."""
         from .launch import GraphedLaunch
 
+        if kwargs.get("workspace") is None:
+            kwargs["workspace"] = self.history.graph_workspace(q.device, kwargs.get("precision", "auto"))
         return GraphedLaunch(lambda: self(q, kv_pages, block_table, kv_current, **kwargs), warmup=warmup)
 
     def __call__(self, q, kv_pages, block_table, kv_current, block_valid_mask=None, *, page_valid_len=None,
                  k_scale: float = 1.0, v_scale: float = 1.0, precision: str = "auto", exp2: str = "fast",
-                 return_lse: bool = False):
+                 return_lse: bool = False, workspace=None):
         out, lse = self.history(q, kv_pages, block_table, block_valid_mask, page_valid_len=page_valid_len,
                                 k_scale=k_scale, v_scale=v_scale, precision=precision, exp2=exp2,
-                                return_lse=True)
+                                return_lse=True, workspace=workspace)
         return self.current(q, kv_current, out, lse, out=out, return_lse=return_lse)

@@ -89,9 +89,12 @@ class HistoryAttentionKernel:
       use ``v_exp_f32``.
 
     * ``splits``: for the e4m3 head_dim-256 kernel, cut the history into this
-      many ranges run by separate workgroups and merged by log-sum-exp (a
-      device workspace is allocated and kept); ``"auto"`` splits only when
-      the (row tile, KV head) workgroups would leave CUs idle.
+      many ranges run by separate workgroups and merged by log-sum-exp;
+      ``"auto"`` splits only when the (row tile, KV head) workgroups would
+      leave CUs idle.  The partial results go to ``workspace`` (a uint8 GPU
+      tensor of ``split_workspace_bytes(splits)`` bytes) or, if none is
+      given, to a workspace the kernel object keeps: split calls through one
+      object that may overlap (other streams) need their own.
     * ``return_lse``: also return each row's log-sum-exp (float32
       ``[pcp, Hq, local_q]``, natural log of the sum of ``exp(score)`` over
       the valid history keys, ``-inf`` for none) - the input of a merge with
@@ -163,6 +166,7 @@ class HistoryAttentionKernel:
         exp2: str = "fast",
         return_lse: bool = False,
         splits="auto",
+        workspace=None,
     ):
         import torch
 
@@ -228,7 +232,10 @@ class HistoryAttentionKernel:
         with torch.cuda.device(device):
             stream = torch.cuda.current_stream(device).cuda_stream
             if n_split > 1:
-                workspace = self._workspace(params, n_split, device)
+                if workspace is None:
+                    workspace = self._workspace(params, n_split, device)
+                elif workspace.dtype != torch.uint8 or workspace.device != device or not workspace.is_contiguous():
+                    raise ValueError(f"workspace must be a contiguous uint8 tensor on {device}")
                 status = self._lib.pcpa_history_attention_split(
                     ctypes.byref(params),
                     n_split,
@@ -261,7 +268,9 @@ class HistoryAttentionKernel:
 
         The output buffer (``out=``, allocated here if not given) and the
         log-sum-exp (``return_lse=True``) are fixed; ``replay()`` recomputes
-        them from the current contents of the same input tensors.
+        them from the current contents of the same input tensors.  A split
+        call gets a workspace of its own, held by the graph, so replays do
+        not share it with eager calls or other graphs.
         """
         import torch
 
@@ -269,6 +278,9 @@ class HistoryAttentionKernel:
 
         if kwargs.get("out") is None:
             kwargs["out"] = torch.empty_like(q)
+        if kwargs.get("workspace") is None:
+            kwargs["workspace"] = self.graph_workspace(q.device, kwargs.get("precision", "auto"),
+                                                       kwargs.get("splits", "auto"))
         page_valid_len = kwargs.pop("page_valid_len", None)
         if page_valid_len is None:
             if block_valid_mask is not None:
@@ -305,12 +317,27 @@ class HistoryAttentionKernel:
         tiles = -(-cfg.actual_history_len // 64)
         return max(1, min(self._native.MAX_SPLITS, -(-cus // items), tiles // self.MIN_TILES_PER_SPLIT))
 
+    def split_workspace_bytes(self, n_split: int) -> int:
+        """Bytes of the workspace of a call with ``n_split`` splits."""
+        size = self._lib.pcpa_split_workspace_bytes(ctypes.byref(self._params(self.config.num_pages, 1.0, 1.0)),
+                                                    n_split)
+        if size < 0:
+            self._native.check(int(size))
+        return int(size)
+
+    def graph_workspace(self, device, precision="auto", splits="auto"):
+        """A new workspace for a call that ``precision``/``splits`` would split, else ``None``."""
+        import torch
+
+        n_split = self.split_count(device, self.uses_bf16_mfma(precision)) if splits == "auto" else int(splits)
+        if n_split <= 1:
+            return None
+        return torch.empty(self.split_workspace_bytes(n_split), dtype=torch.uint8, device=device)
+
     def _workspace(self, params, n_split: int, device):
         import torch
 
-        size = self._lib.pcpa_split_workspace_bytes(ctypes.byref(params), n_split)
-        if size < 0:
-            self._native.check(int(size))
+        size = self.split_workspace_bytes(n_split)
         ws = getattr(self, "_split_ws", None)
         if ws is None or ws.device != device or ws.numel() < size:
             ws = torch.empty(size, dtype=torch.uint8, device=device)

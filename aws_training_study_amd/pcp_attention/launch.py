@@ -22,12 +22,15 @@ class GraphedLaunch:
     ``warmup`` eager calls run first on a side stream (they also allocate any
     workspace the call keeps, outside the capture).  ``result`` is what
     ``fn`` returned during capture; ``replay()`` re-runs the graph on the
-    current stream and returns it.
+    current stream and returns it.  ``fn`` is kept as long as the graph, and
+    with it every tensor it closes over: the recorded kernels address their
+    memory directly.
     """
 
     def __init__(self, fn: Callable[[], Any], warmup: int = 1):
         import torch
 
+        self.fn = fn
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):

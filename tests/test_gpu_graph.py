@@ -61,3 +61,28 @@ def test_graphed_prefill_replays_exactly(cuda_device):
         out = graphed.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"prefill replay {i} differs from the eager call"
+
+
+def test_graph_keeps_its_split_workspace(cuda_device):
+    """A split graph holds its own workspace: eager calls that grow or use the
+    kernel's kept workspace in between leave its replays unchanged."""
+    problem = build_workload_problem("four-chip-fp8", seed=44)
+    gpu = problem.to(cuda_device)
+    kernel = make_history_attention_kernel(problem.config)
+    n_split = kernel.split_count(cuda_device, kernel.uses_bf16_mfma())
+    print(f"case four-chip-fp8: auto splits={n_split}", flush=True)
+    assert n_split > 1
+    kw = dict(page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale, v_scale=problem.v_scale)
+    graphed = kernel.graphed(gpu.q_stacked, gpu.kv_pages, gpu.block_table, **kw)
+    eager = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, **kw)
+    # more splits: the kept workspace is replaced by a larger one
+    wider = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, splits=2 * n_split, **kw)
+    out = graphed.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, eager)
+    assert (wider.float() - eager.float()).abs().max().item() < 2e-2  # same attention, another split
+    # a caller-provided workspace gives the kept one's bits
+    ws = torch.empty(kernel.split_workspace_bytes(n_split), dtype=torch.uint8, device=cuda_device)
+    own = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, workspace=ws, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(own, eager)
