@@ -99,6 +99,12 @@ class KVCacheWriter:
                 continue
             if tuple(t.shape) != table_shape or t.dtype != torch.int32 or not t.is_contiguous() or not t.is_cuda:
                 raise ValueError(f"{name} must be a contiguous int32 GPU tensor {table_shape}")
+        for name, t in (("v", v), ("kv_pages", kv_pages), ("block_table", block_table),
+                        ("page_valid_len", page_valid_len)):
+            if t is not None and t.device != k.device:
+                raise ValueError(f"{name} is on {t.device}, k on {k.device}: all tensors must share one GPU")
+        if k.shape[1] >= 2**31 or not 0 <= int(first_pos) < 2**63:
+            raise ValueError("num_tokens must be below 2^31 and first_pos non-negative")
         params = self._native.PcpaParams(num_pages=kv_pages.shape[0], k_scale=float(k_scale),
                                          v_scale=float(v_scale), **self._static)
         with torch.cuda.device(k.device):
