@@ -110,6 +110,16 @@ def test_python_entry_validates_before_launch():
         kernel(q, torch.zeros(4, 10), torch.zeros(4, 1, dtype=torch.int32))
 
 
+def test_split_workspace_size_from_python():
+    cfg = PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=2048, actual_history_len=2048,
+                             backend="hip")
+    kernel = make_history_attention_kernel(cfg)
+    rows = cfg.pcp_size * cfg.num_q_heads * cfg.local_q_len
+    assert kernel.split_workspace_bytes(3) == 3 * rows * (cfg.head_dim + 1) * 4
+    with pytest.raises(_native.PcpaError, match="BAD_SHAPE"):
+        kernel.split_workspace_bytes(_native.MAX_SPLITS + 1)
+
+
 def test_cache_write_validates_without_a_gpu(lib):
     """pcpa_kv_cache_write / pcpa_absmax_bf16 argument errors come back before any HIP call."""
     p = _good_params()  # pcp 4, Hkv 2, D 64, block 128, 4 local blocks: 512 local slots per rank
