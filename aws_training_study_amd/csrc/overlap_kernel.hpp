@@ -168,15 +168,25 @@ struct Lanes {
     uint32_t dma_v;   // same for V (its own swizzle)
 };
 
-// Tiles j-1 .. j+2 of iteration j.  e < 0: before the first tile;
-// e >= num_entries: after the last (both phantom, valid length 0).
-struct Cursors {
-    TileCursor cm1, c0, c1, c2;
-};
-
 __device__ __forceinline__ bool is_real(const FwdArgs& a, const TileCursor& c) {
     return c.e >= 0 && c.e < a.num_entries;
 }
+
+// Valid keys of a tile for the softmax: its length if real, 0 before the
+// first tile, -1 after the last (phantom tiles; -1 also ends the walk).
+__device__ __forceinline__ int tile_keys(const FwdArgs& a, const TileCursor& c) {
+    return is_real(a, c) ? c.n - c.base : (c.e < 0 ? 0 : -1);
+}
+
+// Tiles j-1 .. j+2 of iteration j.  e < 0: before the first tile;
+// e >= num_entries: after the last (both phantom).  Tiles j+1 and j+2 are
+// still to be loaded and keep their cursors; of tiles j-1 and j only the
+// softmax's valid key counts (tile_keys) are kept, which keeps the loop's
+// scalar registers few.
+struct Cursors {
+    int km1, k0;
+    TileCursor c1, c2;
+};
 
 // Per-lane online-softmax state (log2 domain) and the scratch of the
 // softmax in progress.  l is the full row sum (both lane halves hold it).
@@ -446,17 +456,17 @@ __device__ __forceinline__ void iteration(const FwdArgs& a, uint8_t* lds, int wa
         constexpr int VST = (J4 + 3) % kStages;
         s_half<D, KST, true, VST>(k_addr, v_addr, q, s, xv, pbuf[J4 & 1], sm);
         pv_half<D, VST, true, FAST>(v_addr, xv, o, pbuf[(J4 + 1) & 1], s, pbuf[J4 & 1], sm,
-                              is_real(a, cs.c0) ? cs.c0.n - cs.c0.base : 0, h);
+                              cs.k0, h);
     } else {
         // PV(j-2) beside softmax(j-1), then S(j)
         constexpr int VST = (J4 + 2) % kStages;
         pv_half<D, VST, false, FAST>(v_addr, xv, o, pbuf[J4 & 1], s, pbuf[(J4 + 1) & 1], sm,
-                               is_real(a, cs.cm1) ? cs.cm1.n - cs.cm1.base : 0, h);
+                               cs.km1, h);
         s_half<D, KST, false, 0>(k_addr, v_addr, q, s, xv, pbuf[J4 & 1], sm);
     }
 
-    cs.cm1 = cs.c0;
-    cs.c0 = cs.c1;
+    cs.km1 = cs.k0;
+    cs.k0 = tile_keys(a, cs.c1);
     cs.c1 = cs.c2;
     if (is_real(a, cs.c2)) cs.c2 = next_tile(a, head, cs.c2);
 }
@@ -468,16 +478,16 @@ __device__ __forceinline__ void walk(const FwdArgs& a, uint8_t* lds, int wave, i
                                      v16f (&o)[Shape<D>::DT], SoftmaxRow& sm, Cursors cs, int head) {
     for (;;) {
         // after iteration j the loop ends if tile j-1 was past the last tile
-        bool done = cs.cm1.e >= a.num_entries;
+        bool done = cs.km1 < 0;
         iteration<D, 0, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
         if (done) break;
-        done = cs.cm1.e >= a.num_entries;
+        done = cs.km1 < 0;
         iteration<D, 1, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
         if (done) break;
-        done = cs.cm1.e >= a.num_entries;
+        done = cs.km1 < 0;
         iteration<D, 2, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
         if (done) break;
-        done = cs.cm1.e >= a.num_entries;
+        done = cs.km1 < 0;
         iteration<D, 3, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
         if (done) break;
     }
@@ -609,15 +619,15 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
         __syncthreads();
         const TileCursor before{-1, 0, 0, 0};
         Cursors cs;
-        cs.cm1 = before;
-        cs.c0 = first;
+        cs.km1 = tile_keys(a, before);
+        cs.k0 = tile_keys(a, first);
         cs.c1 = next_tile(a, head, first);
         cs.c2 = is_real(a, cs.c1) ? next_tile(a, head, cs.c1) : cs.c1;
         // K(0), then V(0) and K(1) as if requested at the top of iteration -1.
         if (P::issues(wave)) {
             const int wave_off = P::block(wave) * 1024;
-            load_k<S, P>(a, cs.c0, lds, 0, wave_off, L.dma_k);
-            load_v<S, P>(a, cs.c0, lds, 0, wave_off, L.dma_v, true);
+            load_k<S, P>(a, first, lds, 0, wave_off, L.dma_k);
+            load_v<S, P>(a, first, lds, 0, wave_off, L.dma_v, true);
             if (is_real(a, cs.c1)) load_k<S, P>(a, cs.c1, lds, 1, wave_off, L.dma_k);
         }
         if (wave < kWaves / 2)
