@@ -297,17 +297,21 @@ def paged_history_attention(
     """float64 model of the collapsed page loop.
 
     Reads every (rank, block) page through the block table, keeps its valid
-    prefix, and runs dense attention over the concatenation; ``pool`` rows
-    are ``pack_local_kv`` payloads already decoded to floats.
+    prefix (lengths clamped to [0, block_size]), and runs dense attention
+    over the concatenation; ``pool`` rows are ``pack_local_kv`` payloads
+    already decoded to floats.  Table entries outside ``[0, len(pool))`` are
+    skipped, as the C ABI documents for the kernel (the reference's tables
+    never hold such entries).
     """
     hkv, blk, d = shape.num_kv_heads, shape.block_size, shape.head_dim
     ks, vs = [], []
     for r in range(shape.pcp_size):
         for b in range(shape.max_local_blocks):
-            n = int(valid_len[r, b])
-            if n <= 0:
+            n = min(int(valid_len[r, b]), blk)
+            page_index = int(block_table[r, b])
+            if n <= 0 or not 0 <= page_index < pool.shape[0]:
                 continue
-            page = pool[int(block_table[r, b])].reshape(2, hkv, blk, d)
+            page = pool[page_index].reshape(2, hkv, blk, d)
             ks.append(page[0, :, :n])
             vs.append(page[1, :, :n])
     k = np.concatenate(ks, axis=1) * k_scale

@@ -244,3 +244,39 @@ def test_per_rank_list_input(cuda_device):
     assert torch.equal(listed, stacked)
     with pytest.raises(ValueError, match="per-rank Q shards"):
         kernel(shards[:-1], gpu.kv_pages, gpu.block_table)
+
+
+@pytest.mark.parametrize(
+    "kv_dtype,head_dim,precision,splits",
+    [
+        ("fp8_e4m3fn", 256, "fp8", 1),
+        ("fp8_e4m3fn", 256, "fp8", 3),
+        ("fp8_e4m3fn", 128, "fp8", 1),
+        ("fp8_e4m3fn", 256, "bf16", 1),
+        ("bfloat16", 128, "auto", 1),
+    ],
+)
+def test_skipped_pages_holes_and_clamped_lengths(kv_dtype, head_dim, precision, splits, cuda_device):
+    """Table entries outside [0, num_pages) and zero-length pages drop exactly their keys; lengths
+    beyond the block count the whole block (C ABI contract), against the float64 paged oracle."""
+    from test_oracle import _drop_pages
+
+    cfg = PCPAttentionConfig(
+        pcp_size=4, current_len=256, max_history_len=4096, actual_history_len=4096,
+        block_size=256, interleave_size=64, num_q_heads=8, head_dim=head_dim, backend="hip", kv_dtype=kv_dtype,
+    ).validate()
+    print(f"case {kv_dtype} D={head_dim} precision={precision} splits={splits}", flush=True)
+    problem = build_paged_problem(cfg, seed=13, kv_scale="per_tensor" if kv_dtype != "bfloat16" else "none")
+    shape = orc.OracleShape.from_config(cfg)
+    table, valid, kept = _drop_pages(problem, shape)
+    gpu = problem.to(cuda_device)
+    kernel = make_history_attention_kernel(cfg)
+    out = kernel(gpu.q_stacked, gpu.kv_pages, torch.from_numpy(table).to(cuda_device),
+                 page_valid_len=torch.from_numpy(valid).to(cuda_device), k_scale=problem.k_scale,
+                 v_scale=problem.v_scale, precision=precision, splits=splits)
+    torch.cuda.synchronize()
+    q, k, v = _real_history(problem)
+    qs = np.stack(orc.shard_query(q, shape))
+    expected = np.stack([orc.dense_history_attention(qs[r], k[:, kept], v[:, kept], shape.softmax_scale)
+                         for r in range(shape.pcp_size)])
+    _assert_close(out.float().cpu().numpy(), expected, f"{kv_dtype} D={head_dim} {precision} dropped pages")

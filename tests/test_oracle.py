@@ -150,6 +150,43 @@ def test_paged_model_matches_dense(actual):
     np.testing.assert_allclose(got, orc.expected_stacked(q, k, v, shape), atol=1e-12)
 
 
+def _drop_pages(problem, shape):
+    """Table with two out-of-range entries, a zero-length hole and an over-long length,
+    plus the global positions that stay attended (through the layout maps, not the pages)."""
+    table = problem.block_table.numpy().copy()
+    valid = orc.page_valid_lengths(shape).copy()
+    table[1, 2] = -1
+    table[3, 0] = problem.kv_pages.shape[0]
+    valid[0, 1] = 0
+    valid[2, 3] = 100 * shape.block_size  # clamped to the block
+    dropped = {(1, 2), (3, 0), (0, 1)}
+    kept = [p for p in range(shape.actual_history_len)
+            if (lambda o, lp: (o, lp // shape.block_size) not in dropped)(
+                *orc.owner_and_local_position(p, shape.pcp_size, shape.interleave_size))]
+    return table, valid, np.array(kept)
+
+
+def test_paged_model_skips_out_of_range_pages_and_clamps_lengths():
+    """Entries outside [0, num_pages) and zero lengths drop exactly their block's keys; longer
+    lengths count a whole block (checked against dense attention on the kept positions)."""
+    cfg = PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=4096, actual_history_len=4096,
+                             block_size=256, head_dim=64, num_q_heads=4, backend="hip").validate()
+    from aws_training_study_amd.pcp_attention.workloads import build_paged_problem
+
+    problem = build_paged_problem(cfg, seed=12, kv_scale="per_tensor")
+    shape = orc.OracleShape.from_config(cfg)
+    table, valid, kept = _drop_pages(problem, shape)
+    assert len(kept) == 4096 - 3 * 256
+    pool = orc.decode_e4m3fn(problem.kv_pages.view(torch.uint8).numpy())
+    q = problem.inputs.q.double().numpy()
+    qs = np.stack(orc.shard_query(q, shape))
+    got = orc.paged_history_attention(qs, pool, table, valid, shape, problem.k_scale, problem.v_scale)
+    k = orc.decode_e4m3fn(problem.inputs.k.view(torch.uint8).numpy())[:, kept] * problem.k_scale
+    v = orc.decode_e4m3fn(problem.inputs.v.view(torch.uint8).numpy())[:, kept] * problem.v_scale
+    expected = np.stack([orc.dense_history_attention(qs[r], k, v, shape.softmax_scale) for r in range(4)])
+    np.testing.assert_allclose(got, expected, atol=1e-12)
+
+
 def test_expected_rows_agrees_with_stacked():
     cfg = PCPAttentionConfig(pcp_size=2, current_len=128, max_history_len=1024, actual_history_len=700,
                              block_size=256, head_dim=64, num_q_heads=4, backend="hip").validate()
