@@ -9,9 +9,11 @@
 //
 // Two attention kernels share the data layout and operand maps (common.hpp):
 //   * history_fwd_kernel<D, STORE8, FP8, CAUSAL> (tile_kernel.hpp): 4 waves x
-//     32 rows per workgroup, two workgroups per CU, double-buffered tiles;
-//     every head dim (64, 128, 256) and precision (e4m3 or bf16 MFMAs); with
-//     CAUSAL, the current tokens' causal step and its log-sum-exp merge.
+//     32 rows per workgroup, two workgroups per CU (one for bf16 MFMAs at
+//     head_dim 256), double-buffered tiles where two fit in 64 KB; every head
+//     dim (64, 128, 256) and precision (e4m3 or bf16 MFMAs) other than e4m3
+//     at 256; with CAUSAL, the current tokens' causal step and its
+//     log-sum-exp merge.
 //   * ovl::history_fwd_overlap<256, FAST, LSE, SPLIT> (overlap_kernel.hpp):
 //     the e4m3-MFMA path at head_dim 256, 8 waves x 32 rows, a two-stage
 //     in-wave pipeline with the two waves of a SIMD staggered by half a tile
