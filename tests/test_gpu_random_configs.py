@@ -6,10 +6,13 @@ dtype, MFMA precision and a runtime history length (generally not aligned to
 anything) from a fixed seed, so the set is the same on every run.  Bar:
 max-abs <= 2e-2 and mean-abs <= 2e-3, except that e4m3 MFMAs over short
 histories (where the e4m3 rounding of Q and P is not averaged away) are
-held to the one-pass kernel's own error plus 4e-3 when the bar is missed.
+held to the one-pass kernel's own error (same exp2 mode) plus 4e-3 when the
+bar is missed.
 """
 
 from __future__ import annotations
+
+import os
 
 import numpy as np
 import pytest
@@ -24,7 +27,8 @@ from test_gpu_parity import MAX_ABS_TOL, MEAN_ABS_TOL, _real_history
 
 pytestmark = pytest.mark.gpu
 
-CASES = 16
+# PCPA_RANDOM_CASES widens the sweep (the same first 16 cases, then more).
+CASES = int(os.environ.get("PCPA_RANDOM_CASES", "16"))
 
 
 def _draw(i: int) -> tuple[PCPAttentionConfig, str, dict]:
@@ -81,7 +85,7 @@ def test_random_configuration(i, cuda_device):
         return
     assert kw.get("precision") == "fp8", "BF16 MFMA path outside the bar"
     one = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len,
-                 k_scale=problem.k_scale, v_scale=problem.v_scale, precision="fp8", splits=1)
+                 k_scale=problem.k_scale, v_scale=problem.v_scale, **{**kw, "splits": 1})
     torch.cuda.synchronize()
     one_max, one_mean = orc.max_abs_and_mean_abs(one.float().cpu().numpy(), exp)
     print(f"  short-history e4m3 case: one-pass max_abs={one_max:.3e} mean_abs={one_mean:.3e}", flush=True)
