@@ -20,9 +20,10 @@ struct TileShape {
     static constexpr int GROW = D * (STORE8 ? 1 : 2);  // cache bytes of one key row
     static constexpr int GCHUNKS = GROW / 16;
     static constexpr bool WIDEN = STORE8 && !FP8;
-    // Double-buffered (prefetching) when both buffers fit the 64 KB static
-    // LDS limit; the widening path stages synchronously through registers.
-    static constexpr int NBUF = (!WIDEN && 4 * TILE <= 65536) ? 2 : 1;
+    // Double-buffered (prefetching) when both buffers fit in 128 KB of LDS
+    // (gfx950 has 160 KB per CU); the widening path stages synchronously
+    // through registers.
+    static constexpr int NBUF = (!WIDEN && 4 * TILE <= 131072) ? 2 : 1;
     static constexpr int QK = FP8 ? D / 64 : D / 16;   // k-steps of the score MFMA
     static constexpr int DT = D / 32;                  // 32-row d tiles of O^T
     static constexpr int DMA_PER_WAVE = CHUNKS / 4;    // 1 KB DMA blocks per wave per operand
@@ -261,25 +262,28 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
         // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1): for score
         // tile t and half u, keys 32t + 16u + 8*(grp>>1) + [0, 8) of column
         // d, 4 per transposing read.
+        // The second buffer of a 32 KB tile lies beyond the 16-bit immediate:
+        // its 64 KB part goes into the address.
+        constexpr uint32_t VHI = VBASE & ~0xFFFFu;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-            const uint32_t a0 = L.v_addr[0] ^ ((4 * dt) << 4);
-            const uint32_t a1 = L.v_addr[1] ^ ((4 * dt) << 4);
+            const uint32_t a0 = (L.v_addr[0] ^ ((4 * dt) << 4)) + VHI;
+            const uint32_t a1 = (L.v_addr[1] ^ ((4 * dt) << 4)) + VHI;
             v2i x[4];
-            x[0] = ds_read_tr16_b64<VBASE>(a0);
-            x[1] = ds_read_tr16_b64<VBASE>(a1);
-            x[2] = ds_read_tr16_b64<VBASE + 16 * ROW>(a0);
-            x[3] = ds_read_tr16_b64<VBASE + 16 * ROW>(a1);
+            x[0] = ds_read_tr16_b64<(VBASE) & 0xFFFF>(a0);
+            x[1] = ds_read_tr16_b64<(VBASE) & 0xFFFF>(a1);
+            x[2] = ds_read_tr16_b64<(VBASE + 16 * ROW) & 0xFFFF>(a0);
+            x[3] = ds_read_tr16_b64<(VBASE + 16 * ROW) & 0xFFFF>(a1);
             lds_results_ready(x);
             const v4i aop0 = {x[0][0], x[0][1], x[1][0], x[1][1]};
             const v4i aop1 = {x[2][0], x[2][1], x[3][0], x[3][1]};
             st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop0), pop[0][0], st.o[dt], 0, 0, 0);
             st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop1), pop[0][1], st.o[dt], 0, 0, 0);
             v2i y[4];
-            y[0] = ds_read_tr16_b64<VBASE + 32 * ROW>(a0);
-            y[1] = ds_read_tr16_b64<VBASE + 32 * ROW>(a1);
-            y[2] = ds_read_tr16_b64<VBASE + 48 * ROW>(a0);
-            y[3] = ds_read_tr16_b64<VBASE + 48 * ROW>(a1);
+            y[0] = ds_read_tr16_b64<(VBASE + 32 * ROW) & 0xFFFF>(a0);
+            y[1] = ds_read_tr16_b64<(VBASE + 32 * ROW) & 0xFFFF>(a1);
+            y[2] = ds_read_tr16_b64<(VBASE + 48 * ROW) & 0xFFFF>(a0);
+            y[3] = ds_read_tr16_b64<(VBASE + 48 * ROW) & 0xFFFF>(a1);
             lds_results_ready(y);
             const v4i aop2 = {y[0][0], y[0][1], y[1][0], y[1][1]};
             const v4i aop3 = {y[2][0], y[2][1], y[3][0], y[3][1]};
