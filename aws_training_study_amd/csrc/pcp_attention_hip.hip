@@ -10,7 +10,7 @@
 // Two attention kernels share the data layout and operand maps (common.hpp):
 //   * history_fwd_kernel<D, STORE8, FP8, CAUSAL> (tile_kernel.hpp): 4 waves x
 //     32 rows per workgroup, two workgroups per CU (one for bf16 MFMAs at
-//     head_dim 256), double-buffered tiles where two fit in 64 KB; every head
+//     head_dim 256), double-buffered tiles; every head
 //     dim (64, 128, 256) and precision (e4m3 or bf16 MFMAs) other than e4m3
 //     at 256; with CAUSAL, the current tokens' causal step and its
 //     log-sum-exp merge.
