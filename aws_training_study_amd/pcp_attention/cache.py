@@ -130,7 +130,9 @@ def build_page_pool(config: PCPAttentionConfig, k, v, block_table, *, kv_scale: 
         raise ValueError(f"kv_scale must be 'per_tensor' or 'none', got {kv_scale!r}")
     k_scale = v_scale = 1.0
     if cfg.kv_dtype == "fp8_e4m3fn" and kv_scale == "per_tensor":
-        k_scale, v_scale = device_per_tensor_scale(k), device_per_tensor_scale(v)
+        # both reductions queued, then one synchronisation for the two scales
+        amax_k, amax_v = torch.stack([absmax(k), absmax(v)]).tolist()
+        k_scale, v_scale = per_tensor_scale(amax_k), per_tensor_scale(amax_v)
     pool = torch.zeros((cfg.num_pages, cfg.page_elements), dtype=_torch_kv_dtype(cfg.kv_dtype), device=k.device)
     valid = torch.zeros((cfg.pcp_size, cfg.max_local_blocks), dtype=torch.int32, device=k.device)
     table = block_table.to(device=k.device, dtype=torch.int32).contiguous()
