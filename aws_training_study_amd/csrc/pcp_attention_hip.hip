@@ -283,9 +283,10 @@ int32_t pcpa_absmax_bf16(const void* x, int64_t n, float* amax, void* stream) {
     if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
     if (n == 0) return PCPA_OK;
     // spans of whole 8-element groups (the span start stays 16-byte aligned),
-    // at least 32 KB each, at most 2048 workgroups
+    // at least 32 KB each, at most 256 workgroups (one per CU: a 134 MB
+    // tensor then reads at 5.8 TB/s, against 3.7 TB/s with 2048 workgroups)
     constexpr int64_t kMinSpan = 16384;
-    int64_t span = (n + 2047) / 2048;
+    int64_t span = (n + 255) / 256;
     span = span < kMinSpan ? kMinSpan : (span + 7) / 8 * 8;
     const unsigned blocks = (unsigned)((n + span - 1) / span);
     hipLaunchKernelGGL(pcpa::cache::absmax_kernel, dim3(blocks), dim3(pcpa::cache::kThreads), 0, st,
