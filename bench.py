@@ -168,23 +168,13 @@ def cache_write_bench(args) -> int:
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
     stream = torch.cuda.current_stream(device)
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for begin, end in events:
-        begin.record(stream)
-        step()
-        end.record(stream)
-    torch.cuda.synchronize()
-    wall_s = time.perf_counter() - t0
-    launch_ms = sorted(b.elapsed_time(e) for b, e in events)
+    wall_s, kernel_ms = _timed(step, args.steps, stream)
+    spread = _spread(step, min(args.steps, 20), stream)
     traffic, traffic_source = measured_traffic(f"{workload.name}/cache-write")
     elems = 2 * cfg.num_kv_heads * cfg.actual_history_len * cfg.head_dim
     algo = elems * 2 + elems * (1 if fp8 else 2) + 4 * cfg.num_pages  # read bf16, write pages, table
     ms_per_step = wall_s * 1e3 / args.steps
-    kernel_ms = statistics.fmean(launch_ms)
     result = {
         "metric": "KV-cache write GB/s (BF16 K/V -> paged pool, quantise + scatter), 1 GPU",
         "value": round(algo / (ms_per_step * 1e-3) / 1e9, 1),
@@ -201,8 +191,7 @@ def cache_write_bench(args) -> int:
         "config": {"workload": workload.name, "tokens": cfg.actual_history_len, "kv_heads": cfg.num_kv_heads,
                    "head_dim": cfg.head_dim, "pcp_ranks": cfg.pcp_size, "block_size": cfg.block_size,
                    "interleave": cfg.interleave_size, "kv_dtype": cfg.kv_dtype},
-        "kernel_ms": {"min": round(launch_ms[0], 4), "median": round(statistics.median(launch_ms), 4),
-                      "mean": round(kernel_ms, 4)},
+        "kernel_ms": _kernel_ms(kernel_ms, spread),
         "roofline": {"bound": "hbm", "achieved": round(algo / (kernel_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(algo / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "traffic_source": traffic_source, "algorithmic_bytes": algo},
@@ -234,17 +223,44 @@ def causal_flops(cfg) -> float:
 
 
 def _timed(step, steps, stream):
+    """The timed region: `steps` back-to-back steps between one pair of HIP
+    events on `stream`, synchronised on both sides.  Returns wall seconds and
+    the events' mean milliseconds per step.  (One event pair per step would
+    add ~30 us of queue work to every step on ROCm: 0.18 instead of 0.146 ms
+    per step on the 16-rank workload.)"""
+    import torch
+
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    begin.record(stream)
+    for _ in range(steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, begin.elapsed_time(end) / steps
+
+
+def _spread(step, steps, stream):
+    """Per-step event times (sorted) from a pass after the timed region, each
+    step between its own event pair: the spread of launch times, each
+    including the per-pair event overhead."""
     import torch
 
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
     for begin, end in events:
         begin.record(stream)
         step()
         end.record(stream)
     torch.cuda.synchronize()
-    return time.perf_counter() - t0, sorted(b.elapsed_time(e) for b, e in events)
+    return sorted(b.elapsed_time(e) for b, e in events)
+
+
+def _kernel_ms(mean_ms, spread):
+    p90 = spread[max(0, (9 * len(spread) + 9) // 10 - 1)]
+    return {"mean": round(mean_ms, 4), "per_step_min": round(spread[0], 4),
+            "per_step_median": round(statistics.median(spread), 4), "per_step_p90": round(p90, 4)}
 
 
 def current_bench(args) -> int:
@@ -277,7 +293,8 @@ def current_bench(args) -> int:
     for _ in range(args.warmup):
         step()
     stream = torch.cuda.current_stream(device)
-    wall_s, launch_ms = _timed(step, args.steps, stream)
+    wall_s, kernel_ms = _timed(step, args.steps, stream)
+    spread = _spread(step, min(args.steps, 20), stream)
 
     def prefill_step():
         prefill(gpu.q_stacked, gpu.kv_pages, gpu.block_table, kv_cur, page_valid_len=gpu.page_valid_len,
@@ -288,7 +305,6 @@ def current_bench(args) -> int:
 
     flops = causal_flops(cfg)
     ms_per_step = wall_s * 1e3 / args.steps
-    kernel_ms = statistics.fmean(launch_ms)
     achieved = flops / (kernel_ms * 1e-3) / 1e12
     peak = PEAK_TFLOPS["bfloat16"]
     history_flops = model_flops(cfg)
@@ -308,15 +324,14 @@ def current_bench(args) -> int:
         "config": {"workload": workload.name, "pcp_ranks": cfg.pcp_size, "current_tokens": cfg.current_len,
                    "history_tokens": cfg.actual_history_len, "q_heads": cfg.num_q_heads,
                    "kv_heads": cfg.num_kv_heads, "head_dim": cfg.head_dim, "interleave": cfg.interleave_size},
-        "kernel_ms": {"min": round(launch_ms[0], 4), "median": round(statistics.median(launch_ms), 4),
-                      "mean": round(kernel_ms, 4)},
+        "kernel_ms": _kernel_ms(kernel_ms, spread),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4), "traffic": None,
                      "algorithmic_bytes": 2.0 * (3 * cfg.num_q_heads * cfg.current_len * cfg.head_dim
                                                  + 2 * cfg.num_kv_heads * cfg.current_len * cfg.head_dim)
                      + 2 * 4.0 * cfg.num_q_heads * cfg.current_len},
-        "prefill": {"ms_median": round(statistics.median(prefill_ms), 4),
-                    "tflops": round((history_flops + flops) / (statistics.median(prefill_ms) * 1e-3) / 1e12, 2),
+        "prefill": {"ms": round(prefill_ms, 4),
+                    "tflops": round((history_flops + flops) / (prefill_ms * 1e-3) / 1e12, 2),
                     "what": "history attention with lse + this step, in place"},
     }
     if not args.no_cpu_baseline:
@@ -447,27 +462,16 @@ def main(argv=None) -> int:
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
 
     # Timed region: exactly K steps, synchronised on both sides.
     stream = torch.cuda.current_stream(device)
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for begin, end in events:
-        begin.record(stream)
-        step()
-        end.record(stream)
-    torch.cuda.synchronize()
-    wall_s = time.perf_counter() - t0
-    launch_ms = sorted(b.elapsed_time(e) for b, e in events)
+    wall_s, kernel_ms = _timed(step, args.steps, stream)
+    spread = _spread(step, min(args.steps, 20), stream)
 
     flops = model_flops(cfg)
     ms_per_step = wall_s * 1e3 / args.steps
-    kernel_ms = statistics.fmean(launch_ms)
     peak = PEAK_TFLOPS[cfg.kv_dtype]
     achieved = flops / (kernel_ms * 1e-3) / 1e12
-    p90 = launch_ms[max(0, (9 * len(launch_ms) + 9) // 10 - 1)]
     traffic, traffic_source = (args.traffic_bytes, "--traffic-bytes") if args.traffic_bytes else \
         measured_traffic(workload.name)
 
@@ -497,12 +501,7 @@ def main(argv=None) -> int:
             "kv_dtype": cfg.kv_dtype,
         },
         "pct_peak": round(100.0 * flops / (ms_per_step * 1e-3) / 1e12 / peak, 2),
-        "kernel_ms": {
-            "min": round(launch_ms[0], 4),
-            "median": round(statistics.median(launch_ms), 4),
-            "mean": round(kernel_ms, 4),
-            "p90": round(p90, 4),
-        },
+        "kernel_ms": _kernel_ms(kernel_ms, spread),
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved, 2),
