@@ -189,31 +189,50 @@ int32_t pcpa_history_attention_split(const pcpa_params* p, int32_t splits, const
     if (((uintptr_t)q | (uintptr_t)kv_pages | (uintptr_t)out | (uintptr_t)workspace) & 15u) return PCPA_ERR_MISALIGNED;
     if (((uintptr_t)block_table | (uintptr_t)page_valid_len | (uintptr_t)lse) & 3u) return PCPA_ERR_MISALIGNED;
     if (workspace_bytes < need) return PCPA_ERR_BAD_SHAPE;
-    const bool fp8 = p->kv_dtype == PCPA_DTYPE_FP8_E4M3FN && !(p->flags & PCPA_FLAG_BF16_MFMA);
-    if (!fp8 || p->head_dim != 256) return PCPA_ERR_UNSUPPORTED;
+    const bool store8 = p->kv_dtype == PCPA_DTYPE_FP8_E4M3FN;
+    const bool fp8 = store8 && !(p->flags & PCPA_FLAG_BF16_MFMA);
+    const bool overlap = fp8 && p->head_dim == 256;
+    const int64_t es = store8 ? 1 : 2;
 
     pcpa::FwdArgs a = pcpa::common_args(p, q, out);
     a.kv = (const uint8_t*)kv_pages;
     a.block_table = block_table;
     a.page_valid_len = page_valid_len;
-    a.head_stride = (int64_t)p->block_size * p->head_dim;
+    a.head_stride = (int64_t)p->block_size * p->head_dim * es;
     a.page_stride = 2 * (int64_t)p->num_kv_heads * a.head_stride;
     a.num_entries = p->pcp_size * p->max_local_blocks;
     a.num_pages = p->num_pages;
     a.block_size = p->block_size;
     a.score_scale = p->softmax_scale * p->k_scale * pcpa::kLog2e;
     a.v_scale = p->v_scale;
-    a.row_tiles = (a.rows_per_head + pcpa::ovl::kRowsPerGroup - 1) / pcpa::ovl::kRowsPerGroup;
+    const int rows_per_group = overlap ? pcpa::ovl::kRowsPerGroup : pcpa::kRowsPerGroup;
+    a.row_tiles = (a.rows_per_head + rows_per_group - 1) / rows_per_group;
     a.splits = splits;
     const int64_t rows = (int64_t)p->pcp_size * p->num_q_heads * p->local_q_len;
     a.part_o = (float*)workspace;
     a.part_lse = a.part_o + (int64_t)splits * rows * p->head_dim;
 
     void* args[] = {&a};
-    const void* fn = (p->flags & PCPA_FLAG_EXACT_EXP2) ? (const void*)pcpa::ovl::history_fwd_overlap<256, false, false, true>
-                                                       : (const void*)pcpa::ovl::history_fwd_overlap<256, true, false, true>;
+    const void* fn = nullptr;
+    if (overlap) {
+        fn = (p->flags & PCPA_FLAG_EXACT_EXP2) ? (const void*)pcpa::ovl::history_fwd_overlap<256, false, false, true>
+                                               : (const void*)pcpa::ovl::history_fwd_overlap<256, true, false, true>;
+    } else {
+        switch (p->head_dim * 4 + (store8 ? 2 : 0) + (fp8 ? 1 : 0)) {
+            case 64 * 4 + 3: fn = (const void*)pcpa::history_fwd_kernel<64, true, true, false, true>; break;
+            case 128 * 4 + 3: fn = (const void*)pcpa::history_fwd_kernel<128, true, true, false, true>; break;
+            case 64 * 4 + 2: fn = (const void*)pcpa::history_fwd_kernel<64, true, false, false, true>; break;
+            case 128 * 4 + 2: fn = (const void*)pcpa::history_fwd_kernel<128, true, false, false, true>; break;
+            case 256 * 4 + 2: fn = (const void*)pcpa::history_fwd_kernel<256, true, false, false, true>; break;
+            case 64 * 4: fn = (const void*)pcpa::history_fwd_kernel<64, false, false, false, true>; break;
+            case 128 * 4: fn = (const void*)pcpa::history_fwd_kernel<128, false, false, false, true>; break;
+            case 256 * 4: fn = (const void*)pcpa::history_fwd_kernel<256, false, false, false, true>; break;
+            default: return PCPA_ERR_UNSUPPORTED;
+        }
+    }
     const int items = a.row_tiles * p->num_kv_heads * splits;
-    hipError_t err = hipLaunchKernel(fn, dim3(8 * ((items + 7) / 8)), dim3(pcpa::ovl::kThreads), args, 0,
+    hipError_t err = hipLaunchKernel(fn, dim3(8 * ((items + 7) / 8)),
+                                     dim3(overlap ? pcpa::ovl::kThreads : pcpa::kThreads), args, 0,
                                      (hipStream_t)stream);
     if (err != hipSuccess) return PCPA_ERR_LAUNCH;
     const int d_vec8 = p->head_dim / 8;

@@ -330,8 +330,12 @@ __device__ __forceinline__ void tile_step(const FwdArgs& a, const TileCursor& cu
 // row (rank, token) sees current keys up to its own global position.  The
 // epilogue can then merge the result with a history output (merge_o,
 // merge_lse) by log-sum-exp.
-template <int D, bool STORE8, bool FP8, bool CAUSAL = false>
+// SPLIT: the workgroup walks only its split's share of the table entries
+// and writes a normalised FP32 partial output and log-sum-exp (merged by
+// merge_splits_kernel).
+template <int D, bool STORE8, bool FP8, bool CAUSAL = false, bool SPLIT = false>
 __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_fwd_kernel(FwdArgs a) {
+    static_assert(!(CAUSAL && SPLIT), "the current-token step is not split");
     using S = TileShape<D, STORE8, FP8>;
     constexpr int ROW = S::ROW, CHUNKS = S::CHUNKS, QK = S::QK, DT = S::DT;
 
@@ -346,8 +350,11 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
     // keys) and the keys fit in L2 anyway, so launch the heaviest tiles
     // first, both heads alike, and let the early finishers take the light
     // ones (longest-first balancing over all XCDs).
-    const int items = a.row_tiles * a.num_kv_heads;
-    int head, row_tile;
+    // SPLIT: items run row tile fastest, then split, then KV head, so that an
+    // XCD's workgroups share one (KV head, split) and its pages.
+    const int splits = SPLIT ? a.splits : 1;
+    const int items = a.row_tiles * a.num_kv_heads * splits;
+    int head, row_tile, split = 0;
     if constexpr (CAUSAL) {
         const int item = blockIdx.x;
         if (item >= items) return;
@@ -357,8 +364,14 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
         const int per_xcd = (items + 7) / 8;
         const int item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
         if (item >= items) return;
-        head = item / a.row_tiles;
-        row_tile = item - head * a.row_tiles;
+        row_tile = item % a.row_tiles;
+        head = item / a.row_tiles / splits;
+        split = item / a.row_tiles - head * splits;
+    }
+    int entry_begin = 0;
+    if constexpr (SPLIT) {
+        entry_begin = (int)((int64_t)a.num_entries * split / splits);
+        a.num_entries = (int)((int64_t)a.num_entries * (split + 1) / splits);
     }
 
     const int tid = threadIdx.x;
@@ -491,7 +504,7 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
         }
     };
 
-    TileCursor cur = advance(TileCursor{-1, 0, 0, 0});
+    TileCursor cur = advance(TileCursor{entry_begin - 1, 0, 0, 0});
     if constexpr (S::NBUF == 2) {
         if (cur.e < a.num_entries) stage_tile_async<S, 0>(a, cur, lds, wave, L);
     }
@@ -513,6 +526,22 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
     // sum_k exp(score_k) = l * 2^(m - bias): P was 2^(x - m + bias)
     float lse = l_tot > 0.f ? __logf(l_tot) + (st.m - (FP8 ? kPBiasLog2 : 0.f)) * kLn2 : -INFINITY;
     const int64_t row_index = row_off / (D * 2);
+    if constexpr (SPLIT) {
+        if (row_ok) {
+            const int64_t prow = (int64_t)split * a.rows_per_head * a.num_kv_heads + row_index;
+            float* const po = a.part_o + prow * D;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int d = 32 * dt + 8 * r4 + 4 * h;
+                    *(v4f*)(po + d) = v4f{st.o[dt][4 * r4 + 0] * scale, st.o[dt][4 * r4 + 1] * scale,
+                                          st.o[dt][4 * r4 + 2] * scale, st.o[dt][4 * r4 + 3] * scale};
+                }
+            if (h == 0) a.part_lse[prow] = lse;
+        }
+        return;
+    }
     float hist_weight = 0.f;
     if (CAUSAL && a.merge_o) {
         // out = (e^lse_h O_h + e^lse O) / (e^lse_h + e^lse)

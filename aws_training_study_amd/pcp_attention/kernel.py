@@ -88,10 +88,9 @@ class HistoryAttentionKernel:
       normalisation); ``"exact"`` rounds ``v_exp_f32``.  Other paths always
       use ``v_exp_f32``.
 
-    * ``splits``: for the e4m3 head_dim-256 kernel, cut the history into this
-      many ranges run by separate workgroups and merged by log-sum-exp;
-      ``"auto"`` splits only when the (row tile, KV head) workgroups would
-      leave CUs idle.  The partial results go to ``workspace`` (a uint8 GPU
+    * ``splits``: cut the history into this many ranges of table entries run
+      by separate workgroups and merged by log-sum-exp; ``"auto"`` splits
+      only when the (row tile, KV head) workgroups would leave CUs idle.  The partial results go to ``workspace`` (a uint8 GPU
       tensor of ``split_workspace_bytes(splits)`` bytes) or, if none is
       given, to a workspace the kernel object keeps: split calls through one
       object that may overlap (other streams) need their own.
@@ -294,28 +293,38 @@ class HistoryAttentionKernel:
         return GraphedLaunch(
             lambda: self(q, kv_pages, block_table, page_valid_len=page_valid_len, **kwargs), warmup=warmup)
 
-    # Each workgroup of the e4m3 head_dim-256 kernel takes 256 query rows of
-    # one KV head and a whole CU.
-    ROWS_PER_WORKGROUP = 256
-    # A split should still walk at least this many 64-key tiles.
-    MIN_TILES_PER_SPLIT = 16
+    # Query rows per workgroup and workgroups per CU: the e4m3 head_dim-256
+    # kernel takes 256 rows and a whole CU; the tile kernel 128 rows, two
+    # per CU (one for BF16 MFMAs at head_dim 256).
+    ROWS_PER_WORKGROUP = {"overlap": 256, "tile": 128}
+    # A split should still walk at least this many 64-key tiles (measured on
+    # the MI355X: the overlap kernel's deeper pipeline needs longer ranges).
+    MIN_TILES_PER_SPLIT = {"overlap": 16, "tile": 4}
 
     def split_count(self, device, bf16_mfma: bool) -> int:
-        """History splits for ``splits="auto"``: enough (row tile, KV head,
-        split) workgroups to give every CU one, for the e4m3 head_dim-256
-        kernel; 1 elsewhere or when the row tiles already fill the GPU."""
+        """History splits for ``splits="auto"`` on ``device`` (``auto_splits``)."""
         import torch
 
+        return self.auto_splits(bf16_mfma, torch.cuda.get_device_properties(device).multi_processor_count)
+
+    def auto_splits(self, bf16_mfma: bool, cus: int) -> int:
+        """Enough (row tile, KV head, split) workgroups to fill the workgroup
+        slots of ``cus`` CUs, each split still walking ``MIN_TILES_PER_SPLIT``
+        tiles and holding a table entry; 1 when the row tiles already fill
+        the GPU."""
         cfg = self.config
-        if bf16_mfma or cfg.kv_dtype != "fp8_e4m3fn" or cfg.head_dim != 256:
-            return 1
+        overlap = not bf16_mfma and cfg.kv_dtype == "fp8_e4m3fn" and cfg.head_dim == 256
+        kind = "overlap" if overlap else "tile"
+        per_cu = 1 if overlap or (bf16_mfma and cfg.head_dim == 256) else 2
         rows_per_head = cfg.pcp_size * cfg.local_q_len * (cfg.num_q_heads // cfg.num_kv_heads)
-        items = -(-rows_per_head // self.ROWS_PER_WORKGROUP) * cfg.num_kv_heads
-        cus = torch.cuda.get_device_properties(device).multi_processor_count
-        if items >= cus:
+        items = -(-rows_per_head // self.ROWS_PER_WORKGROUP[kind]) * cfg.num_kv_heads
+        slots = cus * per_cu
+        if items >= slots:
             return 1
         tiles = -(-cfg.actual_history_len // 64)
-        return max(1, min(self._native.MAX_SPLITS, -(-cus // items), tiles // self.MIN_TILES_PER_SPLIT))
+        entries = cfg.pcp_size * cfg.max_local_blocks
+        return max(1, min(self._native.MAX_SPLITS, entries, -(-slots // items),
+                          tiles // self.MIN_TILES_PER_SPLIT[kind]))
 
     def split_workspace_bytes(self, n_split: int) -> int:
         """Bytes of the workspace of a call with ``n_split`` splits."""

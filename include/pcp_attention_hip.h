@@ -143,8 +143,9 @@ int32_t pcpa_history_attention_lse(const pcpa_params* params, const void* q, con
  * `workspace`, and a second launch merges the partials by log-sum-exp into
  * `out` (and `lse`, optional).  Results equal pcpa_history_attention_lse's to
  * rounding.  For a launch whose (row tile, KV head) workgroups would leave
- * CUs idle (one workgroup of 256 rows per CU).  e4m3 MFMA path at head_dim
- * 256 only (else PCPA_ERR_UNSUPPORTED); splits in [1, PCPA_MAX_SPLITS]
+ * CUs idle (256 rows and a CU per workgroup for e4m3 MFMAs at head_dim 256,
+ * else 128 rows, two per CU).  Every cache dtype, precision and head dim of
+ * pcpa_history_attention_lse; splits in [1, PCPA_MAX_SPLITS]
  * (1 = pcpa_history_attention_lse).  workspace: device memory of at least
  * pcpa_split_workspace_bytes(params, splits) bytes, 16-byte aligned; its
  * contents need no initialisation and are left undefined.  The library does

@@ -163,6 +163,24 @@ def test_lse_and_current_entries_validate_without_a_gpu(lib):
     assert c(ctypes.byref(p), 16, 16, 16, None, None, 16, 2, None) == -6        # lse alignment
 
 
+@pytest.mark.parametrize("workload,bf16_mfma,expected", [
+    ("four-chip-fp8", False, 2),        # 128 overlap workgroups of 256 rows for 256 CUs
+    ("full-fp8", False, 1),             # 512 already fill the GPU
+    ("four-chip-fp8", True, 1),         # BF16 MFMAs at head_dim 256: 256 tile workgroups, one per CU
+    ("tiny-gqa4-d64-bf16", True, 8),    # 16 tile workgroups; 32 tiles, at least 4 per split
+    ("gqa8-d128-bf16", True, 1),        # 1024 tile workgroups
+])
+def test_auto_split_counts(workload, bf16_mfma, expected):
+    from aws_training_study_amd.pcp_attention.workloads import get_workload
+
+    kernel = make_history_attention_kernel(get_workload(workload).resolve(1234).with_overrides(backend="hip"))
+    assert kernel.auto_splits(bf16_mfma, cus=256) == expected
+    # never more splits than table entries, and none for a history of a few tiles
+    short = make_history_attention_kernel(PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=2048,
+                                                             actual_history_len=200, backend="hip"))
+    assert short.auto_splits(True, cus=256) == 1
+
+
 def test_split_entry_validates_without_a_gpu(lib):
     """pcpa_split_workspace_bytes / pcpa_history_attention_split errors come back before any HIP call."""
     p = _good_params(kv_dtype=2, head_dim=256)  # 4 ranks x 8 heads x 64 tokens = 2048 rows
@@ -177,6 +195,8 @@ def test_split_entry_validates_without_a_gpu(lib):
     assert f(ctypes.byref(p), 2, 16, 16, 16, 16, 16, None, 16, size - 16, None) == -3       # too small
     assert f(ctypes.byref(p), 2, 16, 16, 16, 16, 16, None, 8, size, None) == -6             # alignment
     assert f(ctypes.byref(p), 2, 16, 16, 16, 16, 16, 2, 16, size, None) == -6               # lse alignment
-    assert f(ctypes.byref(_good_params(head_dim=256)), 2, 16, 16, 16, 16, 16, None, 16, size, None) == -5  # bf16
-    assert f(ctypes.byref(_good_params(kv_dtype=2, head_dim=256, flags=1)), 2, 16, 16, 16, 16, 16, None, 16, size,
-             None) == -5                                                                    # BF16 MFMAs
+    # BF16 caches and BF16 MFMAs split too (tile kernel): their sizes are checked the same way
+    for other in (_good_params(head_dim=128), _good_params(kv_dtype=2, head_dim=256, flags=1)):
+        need = lib.pcpa_split_workspace_bytes(ctypes.byref(other), 4)
+        assert need == 4 * 2048 * (other.head_dim + 1) * 4
+        assert f(ctypes.byref(other), 4, 16, 16, 16, 16, 16, None, 16, need - 16, None) == -3

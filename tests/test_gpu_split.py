@@ -96,3 +96,89 @@ def test_split_unaligned_and_empty_ranges(actual, splits, cuda_device):
     print(f"split max_abs={max_abs:.3e} mean_abs={mean_abs:.3e} (one pass max_abs={one_max:.3e})", flush=True)
     assert max_abs <= max(2e-2, one_max + 4e-3) and mean_abs <= 2e-3
     assert np.abs(out - one).max() <= 1e-2
+
+
+def _small(head_dim, kv_dtype, actual=8000, heads=(16, 4), block=256):
+    return PCPAttentionConfig(pcp_size=4, current_len=512, max_history_len=8192, actual_history_len=actual,
+                              block_size=block, interleave_size=64, num_q_heads=heads[0], num_kv_heads=heads[1],
+                              head_dim=head_dim, kv_dtype=kv_dtype, backend="hip").validate()
+
+
+# (case, config, precision, splits): the tile kernel's instantiations split
+TILE_CASES = [
+    ("tiny-gqa4-d64-bf16", "tiny-gqa4-d64-bf16", "auto", 8),
+    ("bf16-d128", ("small", 128, "bfloat16"), "auto", 5),
+    ("bf16-d64", ("small", 64, "bfloat16"), "auto", 16),
+    ("bf16-d256", ("small", 256, "bfloat16"), "auto", 3),
+    ("e4m3-d128-fp8", ("small", 128, "fp8_e4m3fn"), "fp8", 4),
+    ("e4m3-d64-fp8", ("small", 64, "fp8_e4m3fn"), "fp8", 7),
+    ("e4m3-d128-bf16", ("small", 128, "fp8_e4m3fn"), "bf16", 2),
+    ("e4m3-d256-bf16", ("small", 256, "fp8_e4m3fn"), "bf16", 4),
+]
+
+
+@pytest.mark.parametrize("name,spec,precision,splits", TILE_CASES, ids=[c[0] for c in TILE_CASES])
+def test_tile_kernel_split_matches_oracle_and_one_pass(name, spec, precision, splits, cuda_device):
+    """Split history on the tile kernel (BF16 caches, BF16 MFMAs, e4m3 below head_dim 256)."""
+    if isinstance(spec, str):
+        problem = build_workload_problem(spec, seed=41)
+    else:
+        cfg = _small(spec[1], spec[2])
+        problem = build_paged_problem(cfg, seed=42 + spec[1],
+                                      kv_scale="per_tensor" if spec[2] == "fp8_e4m3fn" else "none")
+    cfg = problem.config
+    print(f"case {name} splits={splits} precision={precision} entries={cfg.pcp_size * cfg.max_local_blocks}",
+          flush=True)
+    gpu = problem.to(cuda_device)
+    kernel = make_history_attention_kernel(cfg)
+
+    def run(n):
+        res = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len,
+                     k_scale=problem.k_scale, v_scale=problem.v_scale, precision=precision, splits=n,
+                     return_lse=True)
+        torch.cuda.synchronize()
+        return res
+
+    out, lse = run(splits)
+    one, one_lse = run(1)
+    q, k, v = _real_history(problem)
+    exp = orc.expected_stacked(q, k, v, orc.OracleShape.from_config(cfg))
+    _assert_close(out.float().cpu().numpy(), exp, f"{name} split {splits}")
+    diff = (out.float() - one.float()).abs()
+    lse_diff = (lse - one_lse).abs()
+    print(f"vs one pass: max {diff.max().item():.3e} mean {diff.mean().item():.3e}; lse max "
+          f"{lse_diff.max().item():.3e}", flush=True)
+    e4m3 = not kernel.uses_bf16_mfma(precision)
+    # each range rounds P against its own running max: BF16 (e4m3) rounding noise apart
+    assert diff.max().item() <= (1e-2 if e4m3 else 2e-3) and diff.mean().item() <= (1e-3 if e4m3 else 2e-4)
+    assert lse_diff.max().item() <= (1e-2 if e4m3 else 2e-3)
+
+
+@pytest.mark.parametrize("actual,splits", [(1, 4), (300, 16), (8192 - 5, 9)])
+def test_tile_kernel_split_unaligned_and_empty_ranges(actual, splits, cuda_device):
+    """BF16 cache: partial pages and ranges with no valid token (lse -inf, merged away)."""
+    cfg = _small(128, "bfloat16", actual=actual)
+    problem = build_paged_problem(cfg, seed=actual, kv_scale="none")
+    print(f"case bf16-d128 actual={actual} splits={splits}", flush=True)
+    gpu = problem.to(cuda_device)
+    kernel = make_history_attention_kernel(cfg)
+    out = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len,
+                 splits=splits).float().cpu().numpy()
+    q, k, v = _real_history(problem)
+    assert np.isfinite(out).all()
+    _assert_close(out, orc.expected_stacked(q, k, v, orc.OracleShape.from_config(cfg)), f"actual {actual}")
+
+
+def test_auto_splits_tile_kernel(cuda_device):
+    """The 4-rank BF16 workload runs 16 tile workgroups: auto splits it, and matches the oracle."""
+    problem = build_workload_problem("tiny-gqa4-d64-bf16", seed=43)
+    kernel = make_history_attention_kernel(problem.config)
+    n = kernel.split_count(cuda_device, bf16_mfma=True)
+    print(f"auto splits: {n}", flush=True)
+    assert n > 1
+    gpu = problem.to(cuda_device)
+    out = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len)
+    torch.cuda.synchronize()
+    q, k, v = _real_history(problem)
+    _assert_close(out.float().cpu().numpy(),
+                  orc.expected_stacked(q, k, v, orc.OracleShape.from_config(problem.config)), "auto split tile")
