@@ -692,14 +692,18 @@ __global__ void __launch_bounds__(256) merge_splits_kernel(const float* part_o, 
     const int64_t row = idx / d_vec8;
     const int d0 = (int)(idx - row * d_vec8) * 8;
     const int D = d_vec8 * 8;
+    // Unrolled, without a branch on empty ranges, so that the loads of
+    // several splits are in flight together (every split wrote a finite
+    // partial: zeros for a range without valid keys).
     float mx = -INFINITY;
+#pragma unroll 8
     for (int sp = 0; sp < splits; ++sp) mx = fmaxf(mx, part_lse[sp * rows + row]);
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float wsum = 0.f;
+#pragma unroll 4
     for (int sp = 0; sp < splits; ++sp) {
         const float l = part_lse[sp * rows + row];
-        if (l == -INFINITY) continue;
-        const float w = __expf(l - mx);
+        const float w = l == -INFINITY ? 0.f : __expf(l - mx);
         wsum += w;
         const float* const src = part_o + (sp * rows + row) * D + d0;
         const v4f lo = *(const v4f*)src, hi = *(const v4f*)(src + 4);
