@@ -470,13 +470,15 @@ def main(argv=None) -> int:
 
     flops = model_flops(cfg)
     ms_per_step = wall_s * 1e3 / args.steps
-    peak = PEAK_TFLOPS[cfg.kv_dtype]
+    fp8 = not kernel.uses_bf16_mfma()
+    peak = PEAK_TFLOPS["fp8_e4m3fn" if fp8 else "bfloat16"]
     achieved = flops / (kernel_ms * 1e-3) / 1e12
     traffic, traffic_source = (args.traffic_bytes, "--traffic-bytes") if args.traffic_bytes else \
         measured_traffic(workload.name)
 
     result = {
-        "metric": METRIC,
+        "metric": METRIC if workload.name == "full-fp8" else
+        f"ms + TFLOP/s (% {'FP8' if fp8 else 'BF16'} MFMA peak), {workload.name} history attention, 1 GPU",
         "value": round(flops / (ms_per_step * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -486,8 +488,10 @@ def main(argv=None) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8_e4m3" if cfg.kv_dtype == "fp8_e4m3fn" else "bf16",
-        "data": "synthetic (seeded N(0,1) BF16 Q, K/V quantised to e4m3 with per-tensor amax/448 scales)",
+        "dtype": "fp8_e4m3" if fp8 else "bf16",
+        "data": "synthetic (seeded N(0,1) BF16 Q, K/V quantised to e4m3 with per-tensor amax/448 scales)" if fp8
+        else "synthetic (seeded N(0,1) BF16 Q/K/V" + (", K with a per-channel factor in [0.5, 2])"
+                                                      if workload.k_prescale == "per_channel" else ")"),
         "config": {
             "workload": workload.name,
             "pcp_ranks": cfg.pcp_size,
