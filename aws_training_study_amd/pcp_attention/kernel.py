@@ -90,10 +90,11 @@ class HistoryAttentionKernel:
 
     * ``splits``: cut the history into this many ranges of table entries run
       by separate workgroups and merged by log-sum-exp; ``"auto"`` splits
-      only when the (row tile, KV head) workgroups would leave CUs idle.  The partial results go to ``workspace`` (a uint8 GPU
-      tensor of ``split_workspace_bytes(splits)`` bytes) or, if none is
-      given, to a workspace the kernel object keeps: split calls through one
-      object that may overlap (other streams) need their own.
+      only when the (row tile, KV head) workgroups would leave CUs idle.
+      The partial results go to ``workspace`` (a uint8 GPU tensor of
+      ``split_workspace_bytes(splits)`` bytes) or, if none is given, to a
+      workspace the kernel object keeps: split calls through one object
+      that may overlap (other streams) need their own.
     * ``return_lse``: also return each row's log-sum-exp (float32
       ``[pcp, Hq, local_q]``, natural log of the sum of ``exp(score)`` over
       the valid history keys, ``-inf`` for none) - the input of a merge with
