@@ -493,6 +493,18 @@ __device__ __forceinline__ void walk(const FwdArgs& a, uint8_t* lds, int wave, i
     }
 }
 
+// Byte offset of query row `row` of KV head `head` (rows past the last are
+// clamped to it) in the stacked [pcp, Hq, local_q, D] bf16 Q and output.
+template <int D>
+__device__ __forceinline__ int64_t query_row_offset(const FwdArgs& a, int row, int head) {
+    const int rowc = row < a.rows_per_head ? row : a.rows_per_head - 1;
+    const int rank = rowc / a.group_rows;
+    const int rem = rowc - rank * a.group_rows;
+    const int head_in_group = rem / a.local_q;
+    const int tok = rem - head_in_group * a.local_q;
+    return ((int64_t)(rank * a.num_q_heads + head * a.group + head_in_group) * a.local_q + tok) * D * 2;
+}
+
 // LSE: also write each row's log-sum-exp (a separate instantiation, so that
 // the plain one keeps its register allocation).
 // SPLIT: the workgroup walks only its split's share of the table entries
@@ -502,7 +514,7 @@ template <int D, bool FAST, bool LSE, bool SPLIT = false>
 __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     using S = Shape<D>;
     constexpr int QK = S::QK, DT = S::DT, ROW = S::ROW, CHUNKS = S::CHUNKS;
-    constexpr int DMAW = LSE || SPLIT ? kWaves : kWaves / 2;
+    constexpr int DMAW = SPLIT ? kWaves : kWaves / 2;
     using P = DmaPlan<D, DMAW>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * S::RING];
 
@@ -532,16 +544,9 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     const int gl = lane & 15;
 
     // ---- this lane's query row and its e4m3 Q^T operand ---------------------
-    const int row = row_tile * kRowsPerGroup + wave * 32 + j;
-    const bool row_ok = row < a.rows_per_head;
-    const int rowc = row_ok ? row : a.rows_per_head - 1;
-    const int rank = rowc / a.group_rows;
-    const int rem = rowc - rank * a.group_rows;
-    const int head_in_group = rem / a.local_q;
-    const int tok = rem - head_in_group * a.local_q;
-    const int64_t row_off =
-        ((int64_t)(rank * a.num_q_heads + head * a.group + head_in_group) * a.local_q + tok) * D * 2;
-    const uint8_t* const qrow = a.q + row_off;
+    const int q_row = row_tile * kRowsPerGroup + wave * 32 + j;
+    const int64_t q_off = query_row_offset<D>(a, q_row, head);
+    const uint8_t* const qrow = a.q + q_off;
 
     v8i q[QK];
     SoftmaxRow sm;
@@ -637,6 +642,14 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     }
 
     // ---- epilogue: O = O^T / l, bf16; log-sum-exp ---------------------------
+    // The row again, from the lane id: kept live through the walk its offset
+    // takes registers there (the plain and log-sum-exp instantiations then
+    // spill; the split ones keep it).
+    const int row = SPLIT ? q_row
+                          : row_tile * kRowsPerGroup + wave * 32 +
+                                (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) & 31);
+    const bool row_ok = row < a.rows_per_head;
+    const int64_t row_off = SPLIT ? q_off : query_row_offset<D>(a, row, head);
     const float scale = sm.l > 0.f ? a.v_scale / sm.l : 0.f;
     // sum_k exp(score_k) = l * 2^(m - 6), less the average overestimate of
     // the linear-mantissa exp2
