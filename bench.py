@@ -225,9 +225,9 @@ def causal_flops(cfg) -> float:
 def _timed(step, steps, stream):
     """The timed region: `steps` back-to-back steps between one pair of HIP
     events on `stream`, synchronised on both sides.  Returns wall seconds and
-    the events' mean milliseconds per step.  (One event pair per step would
-    add ~30 us of queue work to every step on ROCm: 0.18 instead of 0.146 ms
-    per step on the 16-rank workload.)"""
+    the events' mean milliseconds per step.  (One event pair per step adds
+    queue work to every step on ROCm: 0.161 instead of 0.154 ms per step on
+    the 16-rank workload, 37.8 instead of 30.5 us on the 4-rank one.)"""
     import torch
 
     begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
