@@ -254,6 +254,10 @@ def test_per_rank_list_input(cuda_device):
         ("fp8_e4m3fn", 128, "fp8", 1),
         ("fp8_e4m3fn", 256, "bf16", 1),
         ("bfloat16", 128, "auto", 1),
+        # the tile kernel's split ranges over the same holes
+        ("fp8_e4m3fn", 128, "fp8", 4),
+        ("fp8_e4m3fn", 256, "bf16", 3),
+        ("bfloat16", 128, "auto", 5),
     ],
 )
 def test_skipped_pages_holes_and_clamped_lengths(kv_dtype, head_dim, precision, splits, cuda_device):
