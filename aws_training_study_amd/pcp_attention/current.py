@@ -77,7 +77,9 @@ class CurrentAttentionKernel:
             v_scale=1.0,
             flags=0,
         )
-        status = self._lib.pcpa_check_params(ctypes.byref(_native.PcpaParams(**self._static)))
+        # the launch parameters never change: built once, read by every call
+        self._launch_params = _native.PcpaParams(**self._static)
+        status = self._lib.pcpa_check_params(ctypes.byref(self._launch_params))
         if status != _native.PCPA_OK:
             raise ValueError(f"configuration rejected by the HIP kernel: {_native.status_string(status)}")
 
@@ -109,10 +111,9 @@ class CurrentAttentionKernel:
             out = torch.empty(q_shape, dtype=torch.bfloat16, device=device)
         check("out", out, q_shape, torch.bfloat16)
         lse = torch.empty(lse_shape, dtype=torch.float32, device=device) if return_lse else None
-        params = self._native.PcpaParams(**self._static)
         with torch.cuda.device(device):
             status = self._lib.pcpa_current_attention(
-                ctypes.byref(params),
+                ctypes.byref(self._launch_params),
                 cfg.interleave_size,
                 q.data_ptr(),
                 kv_current.data_ptr(),
