@@ -43,7 +43,7 @@ def parse_args(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[1])
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=30)
-    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--workload", default="full-fp8")
     parser.add_argument("--path", choices=("history", "cache-write", "current", "launch"), default="history",
                         help="history: the attention launch (the headline metric); cache-write: the KV-cache "
