@@ -16,7 +16,7 @@ def pytest_configure(config):
 def cuda_device():
     import torch
 
-    # GPU tests fail (never skip) without a GPU: a skipped parity test on the
-    # GPU box would hide a broken kernel.
+    # GPU tests fail (never skip) without a GPU: a skipped parity test on a
+    # machine meant to run them would hide a broken kernel.
     assert torch.cuda.is_available(), "GPU tests need a visible GPU"
     return torch.device("cuda", 0)
