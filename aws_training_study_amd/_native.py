@@ -15,7 +15,7 @@ from pathlib import Path
 LIB_DIR = Path(__file__).resolve().parent / "_lib"
 LIB_NAME = "libpcp_attention_hip.so"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 PCPA_OK = 0
 STATUS_NAMES = {
@@ -29,6 +29,7 @@ STATUS_NAMES = {
     -7: "PCPA_ERR_LAUNCH",
     -8: "PCPA_ERR_TOO_LARGE",
     -9: "PCPA_ERR_BAD_SCALE",
+    -10: "PCPA_ERR_WORKSPACE",
 }
 
 DTYPE_BF16 = 1
@@ -36,6 +37,11 @@ DTYPE_FP8_E4M3FN = 2
 
 FLAG_BF16_MFMA = 1
 FLAG_EXACT_EXP2 = 2
+FLAG_PRECISION_GUARD = 4
+FLAG_TABLE_INT64 = 8
+# Rows whose probability mass sum_k 2^(x_k - m) is below this are recomputed
+# with BF16 MFMAs under FLAG_PRECISION_GUARD (PCPA_GUARD_MIN_MASS).
+GUARD_MIN_MASS = 384.0
 
 MAX_SPLITS = 64
 
@@ -51,6 +57,8 @@ EXPORTED_SYMBOLS = (
     "pcpa_current_attention",
     "pcpa_kv_cache_write",
     "pcpa_absmax_bf16",
+    "pcpa_block_mask_valid_len",
+    "pcpa_page_alloc",
 )
 
 
@@ -145,6 +153,12 @@ def load_library() -> ctypes.CDLL:
     ]
     lib.pcpa_absmax_bf16.restype = ctypes.c_int32
     lib.pcpa_absmax_bf16.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    lib.pcpa_block_mask_valid_len.restype = ctypes.c_int32
+    lib.pcpa_block_mask_valid_len.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                              ctypes.c_void_p, ctypes.c_void_p]
+    lib.pcpa_page_alloc.restype = ctypes.c_int32
+    lib.pcpa_page_alloc.argtypes = [ctypes.POINTER(PcpaParams), ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
+                                    ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
     version = lib.pcpa_abi_version()
     if version != ABI_VERSION:
         raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}; rebuild it")

@@ -37,7 +37,8 @@ __device__ __forceinline__ uint32_t div(uint32_t n, const FastDiv& f) {
 struct WriteArgs {
     const uint8_t* k;   // [Hkv, n, D] bf16
     const uint8_t* v;
-    const int32_t* block_table;
+    const int32_t* block_table;  // int32 entries, or int64 ones as dword pairs (table_shift 1)
+    int32_t table_shift;
     int32_t* page_valid_len;  // optional
     uint8_t* pages;
     int64_t page_stride;      // bytes of one page
@@ -109,7 +110,7 @@ __global__ void __launch_bounds__(kThreads) kv_write_kernel(WriteArgs a, uint32_
     const uint32_t row = head * a.num_tokens + token;
     if (blk >= (uint32_t)a.max_local_blocks) return;  // excluded by the host's capacity check
     const int32_t entry = (int32_t)(owner * a.max_local_blocks + blk);
-    const int32_t page = a.block_table[entry];
+    const int32_t page = table_page(a.block_table, entry, a.table_shift);
     if ((uint32_t)page >= (uint32_t)a.num_pages) return;
     if (a.page_valid_len && head == 0 && chunk == 0) atomicMax(a.page_valid_len + entry, (int32_t)slot + 1);
 
@@ -142,15 +143,24 @@ __global__ void __launch_bounds__(kThreads) kv_write_kernel(WriteArgs a, uint32_
 // ordered like unsigned integers); *out is cleared first by init_kernel.
 __global__ void absmax_init_kernel(uint32_t* out) { *out = 0u; }
 
+// |x| of the two bf16 values of a dword, as their 15-bit magnitude patterns.
+// Non-negative IEEE values order like their bit patterns, and every NaN
+// pattern (exponent all ones, mantissa non-zero) lies above infinity's, so an
+// integer maximum of magnitudes is the float maximum with NaN propagated, as
+// torch's x.abs().max() computes it.
+__device__ __forceinline__ uint32_t abs_bits_max(uint32_t m, uint32_t word) {
+    return max(m, max(word & 0x7fffu, (word >> 16) & 0x7fffu));
+}
+
 // Workgroup b reduces the contiguous span [b * span, (b + 1) * span) with
 // four 16-byte loads in flight per thread, then one atomic per workgroup.
 __global__ void __launch_bounds__(kThreads) absmax_kernel(const uint16_t* x, int64_t n, int64_t span,
                                                           uint32_t* out) {
     constexpr int kVec = 8, kUnroll = 4, kStep = kThreads * kVec;
-    __shared__ float partial[kThreads / 64];
+    __shared__ uint32_t partial[kThreads / 64];
     const int64_t begin = (int64_t)blockIdx.x * span;
     const int64_t end = begin + span < n ? begin + span : n;
-    float m[kUnroll] = {0.f, 0.f, 0.f, 0.f};
+    uint32_t m[kUnroll] = {0u, 0u, 0u, 0u};
     int64_t i = begin + threadIdx.x * kVec;
     for (; i + (kUnroll - 1) * kStep + kVec <= end; i += kUnroll * kStep) {
         v4i raw[kUnroll];
@@ -159,31 +169,25 @@ __global__ void __launch_bounds__(kThreads) absmax_kernel(const uint16_t* x, int
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                m[u] = fmaxf(m[u], fabsf(bf16_bits_to_f32((uint32_t)raw[u][w] & 0xffffu)));
-                m[u] = fmaxf(m[u], fabsf(bf16_bits_to_f32((uint32_t)raw[u][w] >> 16)));
-            }
+            for (int w = 0; w < 4; ++w) m[u] = abs_bits_max(m[u], (uint32_t)raw[u][w]);
     }
     for (; i < end; i += kStep) {
         if (i + kVec <= end) {
             const v4i raw = *(const v4i*)(x + i);
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                m[0] = fmaxf(m[0], fabsf(bf16_bits_to_f32((uint32_t)raw[w] & 0xffffu)));
-                m[0] = fmaxf(m[0], fabsf(bf16_bits_to_f32((uint32_t)raw[w] >> 16)));
-            }
+            for (int w = 0; w < 4; ++w) m[0] = abs_bits_max(m[0], (uint32_t)raw[w]);
         } else {
-            for (int64_t e = i; e < end; ++e) m[0] = fmaxf(m[0], fabsf(bf16_bits_to_f32(x[e])));
+            for (int64_t e = i; e < end; ++e) m[0] = abs_bits_max(m[0], (uint32_t)x[e]);
         }
     }
-    float r = fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]));
+    uint32_t r = max(max(m[0], m[1]), max(m[2], m[3]));
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) r = fmaxf(r, __shfl_xor(r, off));
+    for (int off = 32; off >= 1; off >>= 1) r = max(r, (uint32_t)__shfl_xor((int)r, off));
     if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = r;
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < kThreads / 64; ++w) r = fmaxf(r, partial[w]);
-        atomicMax(out, __float_as_uint(r));
+        for (int w = 1; w < kThreads / 64; ++w) r = max(r, partial[w]);
+        atomicMax(out, r << 16);  // the float bits of the bf16 magnitude
     }
 }
 

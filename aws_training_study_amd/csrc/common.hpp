@@ -38,7 +38,7 @@ constexpr float kPBiasLog2 = 6.0f;
 struct FwdArgs {
     const uint8_t* q;
     const uint8_t* kv;
-    const int32_t* block_table;
+    const int32_t* block_table;  // int32 entries, or int64 ones read as dword pairs (table_shift 1)
     const int32_t* page_valid_len;
     uint8_t* out;
     int64_t page_stride;   // bytes of one page (K and V of every KV head)
@@ -51,6 +51,7 @@ struct FwdArgs {
     int32_t group;
     int32_t num_kv_heads;
     int32_t num_entries;   // pcp * max_local_blocks
+    int32_t table_shift;   // log2 of the table entry size in dwords: 0 (int32) or 1 (int64)
     int32_t num_pages;
     int32_t block_size;
     float score_scale;     // softmax_scale * k_scale * log2(e)
@@ -67,7 +68,28 @@ struct FwdArgs {
     int32_t splits;
     float* part_o;            // [splits, pcp * Hq * local_q, D]
     float* part_lse;          // [splits, pcp * Hq * local_q]
+    float* part_m;            // [splits, pcp * Hq * local_q]: each range's reference max (log2)
+    // Precision guard of the e4m3-MFMA kernels.  guard_out (one byte per
+    // row, [pcp, Hq, local_q]): the e4m3 kernel (or the split merge) writes 1
+    // for a row whose probability mass sum_k 2^(x_k - m) is below
+    // guard_min_mass, else 0.
+    uint8_t* guard_out;
+    float guard_min_mass;
+    // The BF16 fixup of a guarded launch (history_fwd_kernel<..., FIXUP>):
+    // the plan of guard_plan_kernel ([0] listed tiles, [1] mode, then the
+    // list of KV head * row_tiles + row tile ids) and, in sparse mode, the
+    // partials' capacity in tiles (part_o / part_lse hold [splits,
+    // guard_slots * 128] rows).
+    const int32_t* guard_plan;
+    int32_t guard_slots;
 };
+
+// Modes of a guard plan: no flagged row, few flagged tiles (history split
+// across workgroups, partials merged), or many (one pass per tile).
+constexpr int kGuardNone = 0;
+constexpr int kGuardSparse = 1;
+constexpr int kGuardDense = 2;
+constexpr int kGuardPlanHeader = 4;
 
 // ln(E[(1 + f) / 2^f]) for f uniform in [0, 1): how much the linear-mantissa
 // exp2 of the FP8 overlap kernel overestimates a sum of exponentials on
@@ -192,6 +214,14 @@ struct TileCursor {
     int64_t k_off;
 };
 
+// Page of table entry e, or -1 for an int64 entry beyond 32 bits (treated as
+// out of range like any other).
+template <class P>
+__device__ __forceinline__ int table_page(P table, int e, int shift) {
+    const int page = table[e << shift];
+    return shift && table[2 * e + 1] != 0 ? -1 : page;
+}
+
 // The tile after `c`: the next 64 keys of the same page, or the first tile
 // of the next table entry with valid tokens and an in-range page.  Entries
 // whose page index is outside [0, num_pages) are never read.  The table and
@@ -207,10 +237,41 @@ __device__ __forceinline__ TileCursor next_tile(const FwdArgs& a, int head, Tile
     const const_i32_ptr table = (const_i32_ptr)a.block_table;
     const const_i32_ptr lens = (const_i32_ptr)a.page_valid_len;
     for (int e = c.e + 1; e < a.num_entries; ++e) {
-        const int page = table[e];
+        const int page = table_page(table, e, a.table_shift);
         const int n = min(lens[e], a.block_size);
         if (n > 0 && (unsigned)page < (unsigned)a.num_pages)
             return TileCursor{e, 0, n, (int64_t)page * a.page_stride + (int64_t)head * a.head_stride};
+    }
+    return TileCursor{a.num_entries, 0, 0, 0};
+}
+
+// Key tiles of the whole walk (every entry with valid tokens and an in-range
+// page contributes ceil(n / 64)).
+__device__ __forceinline__ int walk_tiles(const FwdArgs& a) {
+    typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+    const const_i32_ptr table = (const_i32_ptr)a.block_table;
+    const const_i32_ptr lens = (const_i32_ptr)a.page_valid_len;
+    int total = 0;
+    for (int e = 0; e < a.num_entries; ++e) {
+        const int page = table_page(table, e, a.table_shift);
+        const int n = min(lens[e], a.block_size);
+        if (n > 0 && (unsigned)page < (unsigned)a.num_pages) total += (n + kKeyTile - 1) / kKeyTile;
+    }
+    return total;
+}
+
+// The cursor of key tile t of the walk (the end cursor past its last tile).
+__device__ __forceinline__ TileCursor cursor_at_tile(const FwdArgs& a, int head, int t) {
+    typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+    const const_i32_ptr table = (const_i32_ptr)a.block_table;
+    const const_i32_ptr lens = (const_i32_ptr)a.page_valid_len;
+    for (int e = 0; e < a.num_entries; ++e) {
+        const int page = table_page(table, e, a.table_shift);
+        const int n = min(lens[e], a.block_size);
+        if (n <= 0 || (unsigned)page >= (unsigned)a.num_pages) continue;
+        const int tiles = (n + kKeyTile - 1) / kKeyTile;
+        if (t < tiles) return TileCursor{e, t * kKeyTile, n, (int64_t)page * a.page_stride + (int64_t)head * a.head_stride};
+        t -= tiles;
     }
     return TileCursor{a.num_entries, 0, 0, 0};
 }

@@ -136,10 +136,10 @@ struct Shape {
 // Who moves the K and V tiles: the last WAVES waves of the workgroup issue
 // the LDS-DMA of every K and V tile and each waits for its own blocks; the
 // barrier after the waits publishes them to all waves.  WAVES = kWaves / 2
-// is the group that runs PV first (one wave per SIMD); with it the plain
-// launches measured about 1% faster than with all eight waves issuing, but
-// the log-sum-exp and split instantiations then spill Q fragments inside
-// the loop, so those keep WAVES = kWaves.
+// is the group that runs PV first (one wave per SIMD); with it the plain and
+// log-sum-exp launches measured about 1% faster than with all eight waves
+// issuing.  The split instantiations spill Q fragments inside the loop with
+// four issuing waves, so they keep WAVES = kWaves.
 template <int D, int WAVES>
 struct DmaPlan {
     static_assert(WAVES == kWaves || WAVES == kWaves / 2, "DMA from all waves or from the late group");
@@ -505,8 +505,9 @@ __device__ __forceinline__ int64_t query_row_offset(const FwdArgs& a, int row, i
     return ((int64_t)(rank * a.num_q_heads + head * a.group + head_in_group) * a.local_q + tok) * D * 2;
 }
 
-// LSE: also write each row's log-sum-exp (a separate instantiation, so that
-// the plain one keeps its register allocation).
+// LSE: also write each row's log-sum-exp and the precision guard's flag
+// (whichever of a.lse / a.guard_out is set; a separate instantiation, so
+// that the plain one keeps its register allocation).
 // SPLIT: the workgroup walks only its split's share of the table entries
 // and writes a normalised FP32 partial output and log-sum-exp (merged by
 // merge_splits_kernel).
@@ -667,11 +668,21 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
                     *(v4f*)(po + d) = v4f{o[dt][4 * r4 + 0] * scale, o[dt][4 * r4 + 1] * scale,
                                           o[dt][4 * r4 + 2] * scale, o[dt][4 * r4 + 3] * scale};
                 }
-            if (h == 0) a.part_lse[prow] = lse;
+            if (h == 0) {
+                a.part_lse[prow] = lse;
+                if (a.part_m) a.part_m[prow] = sm.m;
+            }
         }
         return;
     }
-    if (LSE && row_ok && h == 0) a.lse[row_off / (D * 2)] = lse;
+    if constexpr (LSE) {
+        // the log-sum-exp and/or the precision guard's flag: l / 2^6 is the
+        // row's probability mass sum_k 2^(x_k - m)
+        if (row_ok && h == 0) {
+            if (a.lse) a.lse[row_off / (D * 2)] = lse;
+            if (a.guard_out) a.guard_out[row_off / (D * 2)] = sm.l < a.guard_min_mass * 64.f ? 1 : 0;
+        }
+    }
     if (row_ok) {
         uint8_t* const orow = a.out + row_off;
 #pragma unroll
@@ -698,8 +709,14 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
 // consecutive d).  out = sum_s w_s O_s / sum_s w_s with w_s = e^(lse_s - max),
 // bf16; lse (optional) = max + ln(sum_s w_s).  HBM bound: 4 * D + 4 bytes read
 // per row and split, 2 * D written.
+// Precision guard (guard_out set): the row's probability mass against the
+// largest range reference m_ref = max_s part_m, sum_s l_s 2^(m_s - m_ref) / 2^6
+// = e^(lse + lse_bias - m_ref ln 2) (lse_bias: what the kernel subtracted
+// from its log-sum-exps), compared with min_mass.
 __global__ void __launch_bounds__(256) merge_splits_kernel(const float* part_o, const float* part_lse, int splits,
-                                                           int64_t rows, int d_vec8, uint8_t* out, float* lse_out) {
+                                                           int64_t rows, int d_vec8, uint8_t* out, float* lse_out,
+                                                           const float* part_m, uint8_t* guard_out, float lse_bias,
+                                                           float min_mass) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= rows * d_vec8) return;
     const int64_t row = idx / d_vec8;
@@ -734,7 +751,14 @@ __global__ void __launch_bounds__(256) merge_splits_kernel(const float* part_o, 
         wv[i] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
     }
     *(v4i*)(out + (row * D + d0) * 2) = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
-    if (lse_out && d0 == 0) lse_out[row] = wsum > 0.f ? mx + __logf(wsum) : -INFINITY;
+    const float lse = wsum > 0.f ? mx + __logf(wsum) : -INFINITY;
+    if (lse_out && d0 == 0) lse_out[row] = lse;
+    if (guard_out && d0 == 0) {
+        float m_ref = -INFINITY;
+        for (int sp = 0; sp < splits; ++sp) m_ref = fmaxf(m_ref, part_m[sp * rows + row]);
+        const float mass = wsum > 0.f ? __expf(lse + lse_bias - m_ref * kLn2) : 0.f;
+        guard_out[row] = mass < min_mass ? 1 : 0;
+    }
 }
 
 }  // namespace pcpa

@@ -45,7 +45,9 @@
 // This file holds the C ABI (include/pcp_attention_hip.h).
 #include "cache_kernels.hpp"
 #include "common.hpp"
+#include "guard_kernels.hpp"
 #include "overlap_kernel.hpp"
+#include "paging_kernels.hpp"
 #include "tile_kernel.hpp"
 
 namespace pcpa {
@@ -63,6 +65,201 @@ inline FwdArgs common_args(const pcpa_params* p, const void* q, void* out) {
     a.num_q_heads = p->num_q_heads;
     a.num_kv_heads = p->num_kv_heads;
     return a;
+}
+
+// Workspace of a history launch: split partials (FP32 outputs, log-sum-exps
+// and reference maxima of every range) and, for the precision guard, the
+// row flags, the fixup plan and the fixup's split partials.
+struct WorkspaceLayout {
+    int64_t part_o, part_lse, part_m, flags, plan, gpart_o, gpart_lse, bytes;
+    int32_t guard_splits, guard_slots, tiles_total;
+};
+
+inline bool guarded(const pcpa_params* p) { return (p->flags & PCPA_FLAG_PRECISION_GUARD) != 0; }
+
+inline int64_t align16(int64_t x) { return (x + 15) / 16 * 16; }
+
+inline WorkspaceLayout workspace_layout(const pcpa_params* p, int splits) {
+    const int64_t rows = (int64_t)p->pcp_size * p->num_q_heads * p->local_q_len;
+    WorkspaceLayout w{};
+    if (splits > 1) {
+        w.part_o = 0;
+        w.part_lse = w.part_o + (int64_t)splits * rows * p->head_dim * 4;
+        w.part_m = w.part_lse + (int64_t)splits * rows * 4;
+        w.bytes = w.part_m + (int64_t)splits * rows * 4;
+    }
+    if (guarded(p)) {
+        // fixup: 128-row tiles of the BF16 tile kernel; the history's key
+        // tiles cut into ranges of at least 4 (256 keys), at most 32, so that
+        // a few flagged tiles cost a short walk rather than a whole history's
+        const int64_t entries = (int64_t)p->pcp_size * p->max_local_blocks;
+        const int64_t key_tiles = entries * (p->block_size / kKeyTile);
+        const int64_t rows_per_head = rows / p->num_q_heads * (p->num_q_heads / p->num_kv_heads);
+        w.tiles_total = (int32_t)((rows_per_head + kRowsPerGroup - 1) / kRowsPerGroup * p->num_kv_heads);
+        int64_t gs = key_tiles / 4;
+        gs = gs < 1 ? 1 : gs > 32 ? 32 : gs;
+        w.guard_splits = (int32_t)gs;
+        const int64_t slots = kGuardPartialRows / kRowsPerGroup / gs;
+        w.guard_slots = (int32_t)(slots < w.tiles_total ? slots : w.tiles_total);
+        w.flags = align16(w.bytes);
+        w.plan = align16(w.flags + rows);
+        w.gpart_o = align16(w.plan + (int64_t)(kGuardPlanHeader + w.tiles_total) * 4);
+        const int64_t prow = (int64_t)w.guard_splits * w.guard_slots * kRowsPerGroup;
+        w.gpart_lse = w.gpart_o + prow * p->head_dim * 4;
+        w.bytes = w.gpart_lse + prow * 4;
+    }
+    return w;
+}
+
+// Arguments of the history kernels for one launch (everything but the
+// split and guard fields).
+inline FwdArgs history_args(const pcpa_params* p, const void* q, const void* kv_pages, const void* block_table,
+                            const int32_t* page_valid_len, void* out, float* lse) {
+    const bool store8 = p->kv_dtype == PCPA_DTYPE_FP8_E4M3FN;
+    const int64_t es = store8 ? 1 : 2;
+    FwdArgs a = common_args(p, q, out);
+    a.kv = (const uint8_t*)kv_pages;
+    a.block_table = (const int32_t*)block_table;
+    a.page_valid_len = page_valid_len;
+    a.head_stride = (int64_t)p->block_size * p->head_dim * es;
+    a.page_stride = 2 * (int64_t)p->num_kv_heads * a.head_stride;
+    a.num_entries = p->pcp_size * p->max_local_blocks;
+    a.table_shift = (p->flags & PCPA_FLAG_TABLE_INT64) ? 1 : 0;
+    a.num_pages = p->num_pages;
+    a.block_size = p->block_size;
+    a.score_scale = p->softmax_scale * p->k_scale * kLog2e;
+    a.v_scale = p->v_scale;
+    a.lse = lse;
+    return a;
+}
+
+// The tile kernel instantiation for (head_dim, cache dtype, MFMA precision).
+template <bool SPLIT>
+inline const void* tile_kernel_for(int head_dim, bool store8, bool fp8) {
+    switch (head_dim * 4 + (store8 ? 2 : 0) + (fp8 ? 1 : 0)) {
+        case 64 * 4 + 3: return (const void*)history_fwd_kernel<64, true, true, false, SPLIT>;
+        case 128 * 4 + 3: return (const void*)history_fwd_kernel<128, true, true, false, SPLIT>;
+        case 64 * 4 + 2: return (const void*)history_fwd_kernel<64, true, false, false, SPLIT>;
+        case 128 * 4 + 2: return (const void*)history_fwd_kernel<128, true, false, false, SPLIT>;
+        case 256 * 4 + 2: return (const void*)history_fwd_kernel<256, true, false, false, SPLIT>;
+        case 64 * 4: return (const void*)history_fwd_kernel<64, false, false, false, SPLIT>;
+        case 128 * 4: return (const void*)history_fwd_kernel<128, false, false, false, SPLIT>;
+        case 256 * 4: return (const void*)history_fwd_kernel<256, false, false, false, SPLIT>;
+        default: return nullptr;  // e4m3 MFMAs at head_dim 256 run the overlap kernel
+    }
+}
+
+// One history attention call: `splits` ranges of table entries (1: one
+// pass), then, for a precision-guarded launch on e4m3 MFMAs, the BF16-MFMA
+// pass over the workgroups whose rows the e4m3 pass flagged.
+inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, const void* kv_pages,
+                              const void* block_table, const int32_t* page_valid_len, void* out, float* lse,
+                              void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+    const int32_t st = pcpa_check_params(p);
+    if (st != PCPA_OK) return st;
+    if (splits < 1 || splits > PCPA_MAX_SPLITS) return PCPA_ERR_BAD_SHAPE;
+    if (!q || !kv_pages || !block_table || !page_valid_len || !out) return PCPA_ERR_NULL_POINTER;
+    if (((uintptr_t)q | (uintptr_t)kv_pages | (uintptr_t)out | (uintptr_t)workspace) & 15u)
+        return PCPA_ERR_MISALIGNED;
+    if (((uintptr_t)block_table | (uintptr_t)page_valid_len | (uintptr_t)lse) & 3u) return PCPA_ERR_MISALIGNED;
+    if ((p->flags & PCPA_FLAG_TABLE_INT64) && ((uintptr_t)block_table & 7u)) return PCPA_ERR_MISALIGNED;
+    const bool store8 = p->kv_dtype == PCPA_DTYPE_FP8_E4M3FN;
+    const bool fp8 = store8 && !(p->flags & PCPA_FLAG_BF16_MFMA);
+    const bool overlap = fp8 && p->head_dim == 256;
+    const bool guard = fp8 && guarded(p);
+    const WorkspaceLayout w = workspace_layout(p, splits);
+    if (w.bytes > 0 && (!workspace || workspace_bytes < w.bytes)) return PCPA_ERR_WORKSPACE;
+    uint8_t* const ws = (uint8_t*)workspace;
+    uint8_t* const flags = guard ? ws + w.flags : nullptr;
+    const bool fast = !(p->flags & PCPA_FLAG_EXACT_EXP2);
+
+    FwdArgs a = history_args(p, q, kv_pages, block_table, page_valid_len, out, lse);
+    const int rows_per_group = overlap ? ovl::kRowsPerGroup : kRowsPerGroup;
+    a.row_tiles = (a.rows_per_head + rows_per_group - 1) / rows_per_group;
+    const void* fn = nullptr;
+    if (splits == 1) {
+        a.guard_out = flags;
+        a.guard_min_mass = PCPA_GUARD_MIN_MASS;
+        if (overlap) {
+            // the log-sum-exp instantiation also writes the guard's flags
+            const bool aux = lse || flags;
+            fn = fast ? (aux ? (const void*)ovl::history_fwd_overlap<256, true, true>
+                             : (const void*)ovl::history_fwd_overlap<256, true, false>)
+                      : (aux ? (const void*)ovl::history_fwd_overlap<256, false, true>
+                             : (const void*)ovl::history_fwd_overlap<256, false, false>);
+        } else {
+            fn = tile_kernel_for<false>(p->head_dim, store8, fp8);
+        }
+    } else {
+        a.splits = splits;
+        a.part_o = (float*)(ws + w.part_o);
+        a.part_lse = (float*)(ws + w.part_lse);
+        a.part_m = guard ? (float*)(ws + w.part_m) : nullptr;
+        if (overlap)
+            fn = fast ? (const void*)ovl::history_fwd_overlap<256, true, false, true>
+                      : (const void*)ovl::history_fwd_overlap<256, false, false, true>;
+        else
+            fn = tile_kernel_for<true>(p->head_dim, store8, fp8);
+    }
+    if (!fn) return PCPA_ERR_UNSUPPORTED;
+    void* args[] = {&a};
+    const int items = a.row_tiles * p->num_kv_heads * splits;
+    if (hipLaunchKernel(fn, dim3(8 * ((items + 7) / 8)), dim3(overlap ? ovl::kThreads : kThreads), args, 0, stream) !=
+        hipSuccess)
+        return PCPA_ERR_LAUNCH;
+    if (splits > 1) {
+        const int64_t rows = (int64_t)p->pcp_size * p->num_q_heads * p->local_q_len;
+        const int d_vec8 = p->head_dim / 8;
+        const int64_t threads = rows * d_vec8;
+        hipLaunchKernelGGL(merge_splits_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+                           (const float*)a.part_o, (const float*)a.part_lse, splits, rows, d_vec8, (uint8_t*)out, lse,
+                           (const float*)a.part_m, flags, overlap && fast ? kFastLseBias : 0.f,
+                           (float)PCPA_GUARD_MIN_MASS);
+        if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
+    }
+    if (guard) {
+        // the BF16 fixup of the flagged rows' 128-row tiles (BF16 MFMAs over
+        // the exactly widened cache): plan, fixup, merge of its ranges
+        GuardShape g;
+        g.rows_total = (int64_t)p->pcp_size * p->num_q_heads * p->local_q_len;
+        g.rows_per_head = a.rows_per_head;
+        g.group_rows = a.group_rows;
+        g.local_q = a.local_q;
+        g.num_q_heads = a.num_q_heads;
+        g.group = a.group;
+        g.row_tiles = (a.rows_per_head + kRowsPerGroup - 1) / kRowsPerGroup;
+        g.tiles_total = w.tiles_total;
+        g.max_sparse = w.guard_slots;
+        int32_t* const plan = (int32_t*)(ws + w.plan);
+        hipLaunchKernelGGL(guard_plan_kernel, dim3(1), dim3(kGuardPlanThreads), 0, stream, (const uint8_t*)flags, g,
+                           plan);
+        if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
+        FwdArgs b = history_args(p, q, kv_pages, block_table, page_valid_len, out, lse);
+        b.row_tiles = g.row_tiles;
+        b.guard_plan = plan;
+        b.splits = w.guard_splits;
+        b.guard_slots = w.guard_slots;
+        b.part_o = (float*)(ws + w.gpart_o);
+        b.part_lse = (float*)(ws + w.gpart_lse);
+        void* bargs[] = {&b};
+        const int sparse_items = w.guard_slots * w.guard_splits;
+        const int grid = sparse_items > w.tiles_total ? sparse_items : w.tiles_total;
+        const void* fix = nullptr;
+        switch (p->head_dim) {
+            case 64: fix = (const void*)history_fwd_kernel<64, true, false, false, false, true>; break;
+            case 128: fix = (const void*)history_fwd_kernel<128, true, false, false, false, true>; break;
+            case 256: fix = (const void*)history_fwd_kernel<256, true, false, false, false, true>; break;
+            default: return PCPA_ERR_UNSUPPORTED;
+        }
+        if (hipLaunchKernel(fix, dim3(grid), dim3(kThreads), bargs, 0, stream) != hipSuccess) return PCPA_ERR_LAUNCH;
+        const int d_vec8 = p->head_dim / 8;
+        const int64_t threads = (int64_t)w.guard_slots * kRowsPerGroup * d_vec8;
+        hipLaunchKernelGGL(guard_merge_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+                           (const float*)b.part_o, (const float*)b.part_lse, w.guard_splits, (const int32_t*)plan, g,
+                           d_vec8, (uint8_t*)out, lse);
+        if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
+    }
+    return PCPA_OK;
 }
 
 }  // namespace pcpa
@@ -83,6 +280,7 @@ const char* pcpa_status_string(int32_t status) {
         case PCPA_ERR_LAUNCH: return "HIP kernel launch failed";
         case PCPA_ERR_TOO_LARGE: return "sizes overflow the kernel's index arithmetic";
         case PCPA_ERR_BAD_SCALE: return "scales must be finite and positive";
+        case PCPA_ERR_WORKSPACE: return "workspace missing or smaller than pcpa_split_workspace_bytes";
         default: return "unknown status";
     }
 }
@@ -94,7 +292,9 @@ int32_t pcpa_check_params(const pcpa_params* p) {
         p->local_q_len <= 0 || p->block_size <= 0 || p->max_local_blocks <= 0 || p->num_pages <= 0)
         return PCPA_ERR_BAD_SHAPE;
     if (p->num_q_heads % p->num_kv_heads) return PCPA_ERR_BAD_SHAPE;
-    if (p->flags & ~(uint32_t)(PCPA_FLAG_BF16_MFMA | PCPA_FLAG_EXACT_EXP2)) return PCPA_ERR_BAD_SHAPE;
+    if (p->flags & ~(uint32_t)(PCPA_FLAG_BF16_MFMA | PCPA_FLAG_EXACT_EXP2 | PCPA_FLAG_PRECISION_GUARD |
+                               PCPA_FLAG_TABLE_INT64))
+        return PCPA_ERR_BAD_SHAPE;
     if (p->q_dtype != PCPA_DTYPE_BF16 || p->out_dtype != PCPA_DTYPE_BF16) return PCPA_ERR_BAD_DTYPE;
     if (p->kv_dtype != PCPA_DTYPE_BF16 && p->kv_dtype != PCPA_DTYPE_FP8_E4M3FN) return PCPA_ERR_BAD_DTYPE;
     if (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256) return PCPA_ERR_UNSUPPORTED;
@@ -113,140 +313,31 @@ int32_t pcpa_check_params(const pcpa_params* p) {
 }
 
 int32_t pcpa_history_attention_lse(const pcpa_params* p, const void* q, const void* kv_pages,
-                                   const int32_t* block_table, const int32_t* page_valid_len, void* out,
+                                   const void* block_table, const int32_t* page_valid_len, void* out,
                                    float* lse, void* stream) {
-    const int32_t st = pcpa_check_params(p);
-    if (st != PCPA_OK) return st;
-    if (!q || !kv_pages || !block_table || !page_valid_len || !out) return PCPA_ERR_NULL_POINTER;
-    if (((uintptr_t)q | (uintptr_t)kv_pages | (uintptr_t)out) & 15u) return PCPA_ERR_MISALIGNED;
-    if (((uintptr_t)block_table | (uintptr_t)page_valid_len | (uintptr_t)lse) & 3u) return PCPA_ERR_MISALIGNED;
-
-    const bool store8 = p->kv_dtype == PCPA_DTYPE_FP8_E4M3FN;
-    const bool fp8 = store8 && !(p->flags & PCPA_FLAG_BF16_MFMA);
-    const int64_t es = store8 ? 1 : 2;
-    pcpa::FwdArgs a = pcpa::common_args(p, q, out);
-    a.kv = (const uint8_t*)kv_pages;
-    a.block_table = block_table;
-    a.page_valid_len = page_valid_len;
-    a.head_stride = (int64_t)p->block_size * p->head_dim * es;
-    a.page_stride = 2 * (int64_t)p->num_kv_heads * a.head_stride;
-    a.num_entries = p->pcp_size * p->max_local_blocks;
-    a.num_pages = p->num_pages;
-    a.block_size = p->block_size;
-    a.score_scale = p->softmax_scale * p->k_scale * pcpa::kLog2e;
-    a.v_scale = p->v_scale;
-    a.lse = lse;
-
-    void* args[] = {&a};
-    const void* fn = nullptr;
-    if (fp8 && p->head_dim == 256) {
-        a.row_tiles = (a.rows_per_head + pcpa::ovl::kRowsPerGroup - 1) / pcpa::ovl::kRowsPerGroup;
-        const int oitems = a.row_tiles * p->num_kv_heads;
-        const bool exact = p->flags & PCPA_FLAG_EXACT_EXP2;
-        if (lse)
-            fn = exact ? (const void*)pcpa::ovl::history_fwd_overlap<256, false, true>
-                       : (const void*)pcpa::ovl::history_fwd_overlap<256, true, true>;
-        else
-            fn = exact ? (const void*)pcpa::ovl::history_fwd_overlap<256, false, false>
-                       : (const void*)pcpa::ovl::history_fwd_overlap<256, true, false>;
-        const hipError_t oerr = hipLaunchKernel(fn, dim3(8 * ((oitems + 7) / 8)), dim3(pcpa::ovl::kThreads), args, 0,
-                                                (hipStream_t)stream);
-        return oerr == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
-    }
-    // (e4m3 MFMAs at head_dim 256 took the overlap kernel above)
-    switch (p->head_dim * 4 + (store8 ? 2 : 0) + (fp8 ? 1 : 0)) {
-        case 64 * 4 + 3: fn = (const void*)pcpa::history_fwd_kernel<64, true, true>; break;
-        case 128 * 4 + 3: fn = (const void*)pcpa::history_fwd_kernel<128, true, true>; break;
-        case 64 * 4 + 2: fn = (const void*)pcpa::history_fwd_kernel<64, true, false>; break;
-        case 128 * 4 + 2: fn = (const void*)pcpa::history_fwd_kernel<128, true, false>; break;
-        case 256 * 4 + 2: fn = (const void*)pcpa::history_fwd_kernel<256, true, false>; break;
-        case 64 * 4: fn = (const void*)pcpa::history_fwd_kernel<64, false, false>; break;
-        case 128 * 4: fn = (const void*)pcpa::history_fwd_kernel<128, false, false>; break;
-        case 256 * 4: fn = (const void*)pcpa::history_fwd_kernel<256, false, false>; break;
-        default: return PCPA_ERR_UNSUPPORTED;
-    }
-    const int items = a.row_tiles * p->num_kv_heads;
-    const hipError_t err =
-        hipLaunchKernel(fn, dim3(8 * ((items + 7) / 8)), dim3(pcpa::kThreads), args, 0, (hipStream_t)stream);
-    return err == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
+    return pcpa::history_launch(p, 1, q, kv_pages, block_table, page_valid_len, out, lse, nullptr, 0,
+                                (hipStream_t)stream);
 }
 
 int64_t pcpa_split_workspace_bytes(const pcpa_params* p, int32_t splits) {
     const int32_t st = pcpa_check_params(p);
     if (st != PCPA_OK) return st;
     if (splits < 1 || splits > PCPA_MAX_SPLITS) return PCPA_ERR_BAD_SHAPE;
-    const int64_t rows = (int64_t)p->pcp_size * p->num_q_heads * p->local_q_len;
-    return (int64_t)splits * rows * ((int64_t)p->head_dim + 1) * 4;
+    return pcpa::workspace_layout(p, splits).bytes;
 }
 
 int32_t pcpa_history_attention_split(const pcpa_params* p, int32_t splits, const void* q, const void* kv_pages,
-                                     const int32_t* block_table, const int32_t* page_valid_len, void* out,
+                                     const void* block_table, const int32_t* page_valid_len, void* out,
                                      float* lse, void* workspace, int64_t workspace_bytes, void* stream) {
-    const int64_t need = pcpa_split_workspace_bytes(p, splits);
-    if (need < 0) return (int32_t)need;
-    if (splits == 1) return pcpa_history_attention_lse(p, q, kv_pages, block_table, page_valid_len, out, lse, stream);
-    if (!q || !kv_pages || !block_table || !page_valid_len || !out || !workspace) return PCPA_ERR_NULL_POINTER;
-    if (((uintptr_t)q | (uintptr_t)kv_pages | (uintptr_t)out | (uintptr_t)workspace) & 15u) return PCPA_ERR_MISALIGNED;
-    if (((uintptr_t)block_table | (uintptr_t)page_valid_len | (uintptr_t)lse) & 3u) return PCPA_ERR_MISALIGNED;
-    if (workspace_bytes < need) return PCPA_ERR_BAD_SHAPE;
-    const bool store8 = p->kv_dtype == PCPA_DTYPE_FP8_E4M3FN;
-    const bool fp8 = store8 && !(p->flags & PCPA_FLAG_BF16_MFMA);
-    const bool overlap = fp8 && p->head_dim == 256;
-    const int64_t es = store8 ? 1 : 2;
-
-    pcpa::FwdArgs a = pcpa::common_args(p, q, out);
-    a.kv = (const uint8_t*)kv_pages;
-    a.block_table = block_table;
-    a.page_valid_len = page_valid_len;
-    a.head_stride = (int64_t)p->block_size * p->head_dim * es;
-    a.page_stride = 2 * (int64_t)p->num_kv_heads * a.head_stride;
-    a.num_entries = p->pcp_size * p->max_local_blocks;
-    a.num_pages = p->num_pages;
-    a.block_size = p->block_size;
-    a.score_scale = p->softmax_scale * p->k_scale * pcpa::kLog2e;
-    a.v_scale = p->v_scale;
-    const int rows_per_group = overlap ? pcpa::ovl::kRowsPerGroup : pcpa::kRowsPerGroup;
-    a.row_tiles = (a.rows_per_head + rows_per_group - 1) / rows_per_group;
-    a.splits = splits;
-    const int64_t rows = (int64_t)p->pcp_size * p->num_q_heads * p->local_q_len;
-    a.part_o = (float*)workspace;
-    a.part_lse = a.part_o + (int64_t)splits * rows * p->head_dim;
-
-    void* args[] = {&a};
-    const void* fn = nullptr;
-    if (overlap) {
-        fn = (p->flags & PCPA_FLAG_EXACT_EXP2) ? (const void*)pcpa::ovl::history_fwd_overlap<256, false, false, true>
-                                               : (const void*)pcpa::ovl::history_fwd_overlap<256, true, false, true>;
-    } else {
-        switch (p->head_dim * 4 + (store8 ? 2 : 0) + (fp8 ? 1 : 0)) {
-            case 64 * 4 + 3: fn = (const void*)pcpa::history_fwd_kernel<64, true, true, false, true>; break;
-            case 128 * 4 + 3: fn = (const void*)pcpa::history_fwd_kernel<128, true, true, false, true>; break;
-            case 64 * 4 + 2: fn = (const void*)pcpa::history_fwd_kernel<64, true, false, false, true>; break;
-            case 128 * 4 + 2: fn = (const void*)pcpa::history_fwd_kernel<128, true, false, false, true>; break;
-            case 256 * 4 + 2: fn = (const void*)pcpa::history_fwd_kernel<256, true, false, false, true>; break;
-            case 64 * 4: fn = (const void*)pcpa::history_fwd_kernel<64, false, false, false, true>; break;
-            case 128 * 4: fn = (const void*)pcpa::history_fwd_kernel<128, false, false, false, true>; break;
-            case 256 * 4: fn = (const void*)pcpa::history_fwd_kernel<256, false, false, false, true>; break;
-            default: return PCPA_ERR_UNSUPPORTED;
-        }
-    }
-    const int items = a.row_tiles * p->num_kv_heads * splits;
-    hipError_t err = hipLaunchKernel(fn, dim3(8 * ((items + 7) / 8)),
-                                     dim3(overlap ? pcpa::ovl::kThreads : pcpa::kThreads), args, 0,
-                                     (hipStream_t)stream);
-    if (err != hipSuccess) return PCPA_ERR_LAUNCH;
-    const int d_vec8 = p->head_dim / 8;
-    const int64_t threads = rows * d_vec8;
-    hipLaunchKernelGGL(pcpa::merge_splits_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                       (hipStream_t)stream, (const float*)a.part_o, (const float*)a.part_lse, splits, rows, d_vec8,
-                       (uint8_t*)out, lse);
-    return hipGetLastError() == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
+    return pcpa::history_launch(p, splits, q, kv_pages, block_table, page_valid_len, out, lse, workspace,
+                                workspace_bytes, (hipStream_t)stream);
 }
 
 int32_t pcpa_history_attention(const pcpa_params* p, const void* q, const void* kv_pages,
-                               const int32_t* block_table, const int32_t* page_valid_len, void* out,
+                               const void* block_table, const int32_t* page_valid_len, void* out,
                                void* stream) {
-    return pcpa_history_attention_lse(p, q, kv_pages, block_table, page_valid_len, out, nullptr, stream);
+    return pcpa::history_launch(p, 1, q, kv_pages, block_table, page_valid_len, out, nullptr, nullptr, 0,
+                                (hipStream_t)stream);
 }
 
 int32_t pcpa_current_attention(const pcpa_params* p, int32_t interleave, const void* q, const void* kv_current,
@@ -314,7 +405,7 @@ int32_t pcpa_absmax_bf16(const void* x, int64_t n, float* amax, void* stream) {
 }
 
 int32_t pcpa_kv_cache_write(const pcpa_params* p, int32_t interleave, int64_t first_pos, int32_t num_tokens,
-                            const void* k, const void* v, const int32_t* block_table, void* kv_pages,
+                            const void* k, const void* v, const void* block_table, void* kv_pages,
                             int32_t* page_valid_len, void* stream) {
     const int32_t st = pcpa_check_params(p);
     if (st != PCPA_OK) return st;
@@ -322,6 +413,7 @@ int32_t pcpa_kv_cache_write(const pcpa_params* p, int32_t interleave, int64_t fi
     if (interleave <= 0 || first_pos < 0 || num_tokens < 0) return PCPA_ERR_BAD_SHAPE;
     if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)kv_pages) & 15u) return PCPA_ERR_MISALIGNED;
     if (((uintptr_t)block_table | (uintptr_t)page_valid_len) & 3u) return PCPA_ERR_MISALIGNED;
+    if ((p->flags & PCPA_FLAG_TABLE_INT64) && ((uintptr_t)block_table & 7u)) return PCPA_ERR_MISALIGNED;
     if (num_tokens == 0) return PCPA_OK;
     // Every position must have a cache block: local index < max_local_blocks *
     // block_size.  The local index grows with the position for each owner
@@ -343,7 +435,8 @@ int32_t pcpa_kv_cache_write(const pcpa_params* p, int32_t interleave, int64_t fi
     pcpa::cache::WriteArgs a;
     a.k = (const uint8_t*)k;
     a.v = (const uint8_t*)v;
-    a.block_table = block_table;
+    a.block_table = (const int32_t*)block_table;
+    a.table_shift = (p->flags & PCPA_FLAG_TABLE_INT64) ? 1 : 0;
     a.page_valid_len = page_valid_len;
     a.pages = (uint8_t*)kv_pages;
     a.head_stride = (int64_t)p->block_size * p->head_dim * es;
@@ -380,6 +473,48 @@ int32_t pcpa_kv_cache_write(const pcpa_params* p, int32_t interleave, int64_t fi
         hipLaunchKernelGGL((pcpa::cache::kv_write_kernel<false, true>), grid, block, 0, hs, a, row_chunks);
     else
         hipLaunchKernelGGL((pcpa::cache::kv_write_kernel<false, false>), grid, block, 0, hs, a, row_chunks);
+    return hipGetLastError() == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
+}
+
+int32_t pcpa_block_mask_valid_len(const void* mask, int32_t pcp_size, int32_t max_local_blocks, int32_t block_size,
+                                  int32_t* page_valid_len, void* stream) {
+    if (!mask || !page_valid_len) return PCPA_ERR_NULL_POINTER;
+    if (pcp_size <= 0 || max_local_blocks <= 0 || block_size <= 0 || block_size % 128) return PCPA_ERR_BAD_SHAPE;
+    if ((int64_t)pcp_size * max_local_blocks > INT32_MAX) return PCPA_ERR_TOO_LARGE;
+    if (((uintptr_t)mask & 1u) || ((uintptr_t)page_valid_len & 3u)) return PCPA_ERR_MISALIGNED;
+    hipLaunchKernelGGL(pcpa::paging::mask_lengths_kernel, dim3(max_local_blocks), dim3(pcpa::paging::kMaskThreads), 0,
+                       (hipStream_t)stream, (const uint16_t*)mask, block_size, max_local_blocks, pcp_size,
+                       page_valid_len);
+    return hipGetLastError() == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
+}
+
+int32_t pcpa_page_alloc(const pcpa_params* p, int32_t interleave, int64_t first_pos, int32_t num_tokens,
+                        void* block_table, const int32_t* free_pages, int32_t* free_count, void* stream) {
+    const int32_t st = pcpa_check_params(p);
+    if (st != PCPA_OK) return st;
+    if (!block_table || !free_pages || !free_count) return PCPA_ERR_NULL_POINTER;
+    if (interleave <= 0 || first_pos < 0 || num_tokens < 0) return PCPA_ERR_BAD_SHAPE;
+    if (((uintptr_t)block_table | (uintptr_t)free_pages | (uintptr_t)free_count) & 3u) return PCPA_ERR_MISALIGNED;
+    if ((p->flags & PCPA_FLAG_TABLE_INT64) && ((uintptr_t)block_table & 7u)) return PCPA_ERR_MISALIGNED;
+    if (num_tokens == 0) return PCPA_OK;
+    // the positions must fit the cache (as pcpa_kv_cache_write requires);
+    // rank 0 owns the most positions of any prefix of the history
+    const int64_t end = first_pos + num_tokens;
+    const int64_t capacity = (int64_t)p->max_local_blocks * p->block_size;
+    if (pcpa::paging::owned_below(end, 0, p->pcp_size, interleave) > capacity) return PCPA_ERR_BAD_SHAPE;
+    pcpa::paging::AllocArgs a;
+    a.table = (int32_t*)block_table;
+    a.table_shift = (p->flags & PCPA_FLAG_TABLE_INT64) ? 1 : 0;
+    a.free_pages = free_pages;
+    a.free_count = free_count;
+    a.first_pos = first_pos;
+    a.end_pos = end;
+    a.pcp = p->pcp_size;
+    a.interleave = interleave;
+    a.block_size = p->block_size;
+    a.max_local_blocks = p->max_local_blocks;
+    hipLaunchKernelGGL(pcpa::paging::page_alloc_kernel, dim3(1), dim3(pcpa::paging::kAllocThreads), 0,
+                       (hipStream_t)stream, a);
     return hipGetLastError() == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
 }
 

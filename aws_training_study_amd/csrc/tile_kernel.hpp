@@ -127,8 +127,8 @@ __device__ __forceinline__ void zero_masked_v(uint8_t* lds_v, int valid, int tid
 }
 
 // Online-softmax state of one lane: running max (log2 domain, times the
-// lane's score factor), this lane half's share of the running sum, and the
-// O^T accumulator tiles.
+// lane's score factor), the running sum (BF16 MFMAs: this lane half's share;
+// e4m3 MFMAs: the whole row's), and the O^T accumulator tiles.
 template <class S>
 struct SoftmaxState {
     float m;
@@ -203,9 +203,12 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
         for (int r = 0; r < 16; ++r) {
             const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], cscale, shift));
             s[t][r] = p;
-            psum += p;
+            if constexpr (!FP8) psum += p;
         }
-    st.l += psum;
+    // BF16: this lane half's share of the row sum, from the unrounded P (the
+    // bf16 rounding of P below is 2^-9 relative).  FP8: the full row sum of
+    // the e4m3-rounded P that the PV MFMAs consume, taken by an MFMA below.
+    if constexpr (!FP8) st.l += psum;
 
     // ---- O^T += V^T . P^T -----------------------------------------------
     if constexpr (FP8) {
@@ -221,6 +224,14 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
                 pk = __builtin_amdgcn_cvt_pk_fp8_f32(s[t][4 * q4 + 2], s[t][4 * q4 + 3], pk, true);
                 pop[4 * t + q4] = pk;
             }
+        // ones (e4m3 1.0) x P^T puts sum_k P[k][q] in every accumulator of
+        // query column q, in both lane halves: the sum of exactly the e4m3
+        // probabilities the PV MFMAs weigh V with, so the output weights sum
+        // to one.
+        int one = 0x38383838;
+        asm volatile("" : "+v"(one));
+        const v8i ones = {one, one, one, one, one, one, one, one};
+        v16f rowsum = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, pop, v16f{}, 0, 0, 0, 0, 0, 0);
         // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1): keys
         // 32*(grp>>1) + [0, 32) of column d, 8 per transposing read; the
         // d tiles are read two at a time, one pair ahead of the MFMAs.
@@ -251,6 +262,11 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
                     __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, pop, st.o[2 * pair + k], 0, 0, 0, 0, 0, 0);
             }
         }
+        // All 16 row-sum registers stay allocated until here: the inline-asm
+        // LDS reads above are invisible to the MFMA hazard checks and must not
+        // be given registers the in-flight MFMA is still going to write.
+        asm volatile("" : "+v"(rowsum));
+        st.l += rowsum[0];
     } else {
         v8bf pop[2][2];
 #pragma unroll
@@ -333,9 +349,16 @@ __device__ __forceinline__ void tile_step(const FwdArgs& a, const TileCursor& cu
 // SPLIT: the workgroup walks only its split's share of the table entries
 // and writes a normalised FP32 partial output and log-sum-exp (merged by
 // merge_splits_kernel).
-template <int D, bool STORE8, bool FP8, bool CAUSAL = false, bool SPLIT = false>
+// FIXUP: the BF16-MFMA pass of a precision-guarded launch.  The plan
+// (guard_plan_kernel) lists the 128-row tiles holding a row the e4m3 pass
+// flagged; in sparse mode workgroup b takes listed tile b / splits and walks
+// history range b % splits into the guard partials (merged by
+// guard_merge_kernel), in dense mode it takes listed tile b and writes the
+// output directly; unlisted workgroups exit at once.
+template <int D, bool STORE8, bool FP8, bool CAUSAL = false, bool SPLIT = false, bool FIXUP = false>
 __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_fwd_kernel(FwdArgs a) {
     static_assert(!(CAUSAL && SPLIT), "the current-token step is not split");
+    static_assert(!FIXUP || (!FP8 && !CAUSAL && !SPLIT), "the guard's fixup runs BF16 MFMAs, one launch");
     using S = TileShape<D, STORE8, FP8>;
     constexpr int ROW = S::ROW, CHUNKS = S::CHUNKS, QK = S::QK, DT = S::DT;
 
@@ -352,10 +375,26 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
     // ones (longest-first balancing over all XCDs).
     // SPLIT: items run row tile fastest, then split, then KV head, so that an
     // XCD's workgroups share one (KV head, split) and its pages.
-    const int splits = SPLIT ? a.splits : 1;
+    int splits = SPLIT ? a.splits : 1;
     const int items = a.row_tiles * a.num_kv_heads * splits;
-    int head, row_tile, split = 0;
-    if constexpr (CAUSAL) {
+    int head, row_tile, split = 0, slot = 0;
+    bool sparse = false;
+    if constexpr (FIXUP) {
+        const int listed = a.guard_plan[0], mode = a.guard_plan[1];
+        sparse = mode == kGuardSparse;
+        if (sparse) {
+            if ((int)blockIdx.x >= listed * a.splits) return;
+            splits = a.splits;
+            slot = blockIdx.x / splits;
+            split = blockIdx.x - slot * splits;
+        } else {
+            if (mode != kGuardDense || (int)blockIdx.x >= listed) return;
+            slot = blockIdx.x;
+        }
+        const int tile_id = a.guard_plan[kGuardPlanHeader + slot];
+        head = tile_id / a.row_tiles;
+        row_tile = tile_id - head * a.row_tiles;
+    } else if constexpr (CAUSAL) {
         const int item = blockIdx.x;
         if (item >= items) return;
         head = item % a.num_kv_heads;
@@ -372,6 +411,14 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
     if constexpr (SPLIT) {
         entry_begin = (int)((int64_t)a.num_entries * split / splits);
         a.num_entries = (int)((int64_t)a.num_entries * (split + 1) / splits);
+    }
+    // FIXUP, sparse: range `split` of `splits` equal ranges of the walk's key
+    // tiles (not of table entries: short ranges even for a few large pages)
+    int tile_first = 0, tiles_left = -1;
+    if (FIXUP && sparse) {
+        const int total = walk_tiles(a);
+        tile_first = (int)((int64_t)total * split / splits);
+        tiles_left = (int)((int64_t)total * (split + 1) / splits) - tile_first;
     }
 
     const int tid = threadIdx.x;
@@ -500,11 +547,16 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
             const TileCursor n = next_current_tile(a, head, c);
             return n.base < group_limit ? n : TileCursor{a.num_entries, 0, 0, 0};
         } else {
+            if (FIXUP && tiles_left >= 0 && --tiles_left <= 0) return TileCursor{a.num_entries, 0, 0, 0};
             return next_tile(a, head, c);
         }
     };
 
-    TileCursor cur = advance(TileCursor{entry_begin - 1, 0, 0, 0});
+    TileCursor cur;
+    if (FIXUP && sparse)
+        cur = tiles_left > 0 ? cursor_at_tile(a, head, tile_first) : TileCursor{a.num_entries, 0, 0, 0};
+    else
+        cur = advance(TileCursor{entry_begin - 1, 0, 0, 0});
     if constexpr (S::NBUF == 2) {
         if (cur.e < a.num_entries) stage_tile_async<S, 0>(a, cur, lds, wave, L);
     }
@@ -521,14 +573,17 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
     }
 
     // ---- epilogue: O = O^T / l, bf16; log-sum-exp; merge -------------------
-    const float l_tot = halves_sum(st.l);
+    // (FP8: st.l is already the whole row's sum, in both lane halves)
+    const float l_tot = FP8 ? st.l : halves_sum(st.l);
     float scale = l_tot > 0.f ? a.v_scale / l_tot : 0.f;
     // sum_k exp(score_k) = l * 2^(m - bias): P was 2^(x - m + bias)
     float lse = l_tot > 0.f ? __logf(l_tot) + (st.m - (FP8 ? kPBiasLog2 : 0.f)) * kLn2 : -INFINITY;
     const int64_t row_index = row_off / (D * 2);
-    if constexpr (SPLIT) {
+    if (FIXUP && sparse) {
+        // guard partials [splits, slots * 128, D]: slot rows in tile order
         if (row_ok) {
-            const int64_t prow = (int64_t)split * a.rows_per_head * a.num_kv_heads + row_index;
+            const int64_t prow = (int64_t)split * a.guard_slots * kRowsPerGroup + (int64_t)slot * kRowsPerGroup +
+                                 wave * kRowsPerWave + j;
             float* const po = a.part_o + prow * D;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt)
@@ -542,6 +597,29 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
         }
         return;
     }
+    if constexpr (SPLIT) {
+        if (row_ok) {
+            const int64_t prow = (int64_t)split * a.rows_per_head * a.num_kv_heads + row_index;
+            float* const po = a.part_o + prow * D;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int d = 32 * dt + 8 * r4 + 4 * h;
+                    *(v4f*)(po + d) = v4f{st.o[dt][4 * r4 + 0] * scale, st.o[dt][4 * r4 + 1] * scale,
+                                          st.o[dt][4 * r4 + 2] * scale, st.o[dt][4 * r4 + 3] * scale};
+                }
+            if (h == 0) {
+                a.part_lse[prow] = lse;
+                if (a.part_m) a.part_m[prow] = st.m;
+            }
+        }
+        return;
+    }
+    // Precision guard (e4m3 MFMAs): l / 2^6 is the row's probability mass
+    // sum_k 2^(x_k - m) against the running reference.
+    if (FP8 && a.guard_out && row_ok && h == 0)
+        a.guard_out[row_index] = st.l < a.guard_min_mass * 64.f ? 1 : 0;
     float hist_weight = 0.f;
     if (CAUSAL && a.merge_o) {
         // out = (e^lse_h O_h + e^lse O) / (e^lse_h + e^lse)

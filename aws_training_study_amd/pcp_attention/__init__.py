@@ -7,7 +7,7 @@ kernel entry points, the paged-pool helpers, the KV-cache producer and the
 current-token step.
 """
 
-from .cache import KVCacheWriter, absmax, build_page_pool
+from .cache import KVCacheWriter, PageAllocator, absmax, append_history, build_page_pool
 from .config import PCPAttentionConfig, get_preset
 from .current import CurrentAttentionKernel, PrefillAttention, stack_current_kv
 from .kernel import make_history_attention_kernel, pack_local_kv, wrap_for_native_torch
@@ -28,7 +28,9 @@ __all__ = [
     "GraphedLaunch",
     "KVCacheWriter",
     "PCPAttentionConfig",
+    "PageAllocator",
     "absmax",
+    "append_history",
     "build_page_pool",
     "gather_history",
     "get_preset",

@@ -50,8 +50,9 @@ class KVCacheWriter:
     v_scale=1.0, page_valid_len=None)``: ``k``/``v`` are contiguous BF16
     ``[Hkv, n, D]`` GPU tensors holding the tokens at global positions
     ``first_pos .. first_pos + n - 1``; ``kv_pages`` is the config's
-    ``[num_pages, page_elements]`` pool; ``block_table`` int32 ``[pcp,
-    max_local_blocks]``.  An e4m3 pool stores ``x / scale`` rounded to e4m3;
+    ``[num_pages, page_elements]`` pool; ``block_table`` int32 or int64
+    ``[pcp, max_local_blocks]`` (entries outside ``[0, num_pages)`` are not
+    written).  An e4m3 pool stores ``x / scale`` rounded to e4m3;
     a BF16 pool stores ``x``.  ``page_valid_len`` (int32, optional) is
     raised to cover every written token.  Asynchronous on the current stream.
     """
@@ -94,11 +95,13 @@ class KVCacheWriter:
                 or kv_pages.dtype != _torch_kv_dtype(cfg.kv_dtype) or not kv_pages.is_contiguous()):
             raise ValueError(f"kv_pages must be a contiguous {cfg.kv_dtype} [num_pages, {cfg.page_elements}] pool")
         table_shape = (cfg.pcp_size, cfg.max_local_blocks)
-        for name, t in (("block_table", block_table), ("page_valid_len", page_valid_len)):
+        for name, t, dtypes in (("block_table", block_table, (torch.int32, torch.int64)),
+                                ("page_valid_len", page_valid_len, (torch.int32,))):
             if t is None:
                 continue
-            if tuple(t.shape) != table_shape or t.dtype != torch.int32 or not t.is_contiguous() or not t.is_cuda:
-                raise ValueError(f"{name} must be a contiguous int32 GPU tensor {table_shape}")
+            if tuple(t.shape) != table_shape or t.dtype not in dtypes or not t.is_contiguous() or not t.is_cuda:
+                raise ValueError(f"{name} must be a contiguous {' or '.join(str(d) for d in dtypes)} GPU tensor "
+                                 f"{table_shape}")
         for name, t in (("v", v), ("kv_pages", kv_pages), ("block_table", block_table),
                         ("page_valid_len", page_valid_len)):
             if t is not None and t.device != k.device:
@@ -107,6 +110,8 @@ class KVCacheWriter:
             raise ValueError("num_tokens must be below 2^31 and first_pos non-negative")
         params = self._native.PcpaParams(num_pages=kv_pages.shape[0], k_scale=float(k_scale),
                                          v_scale=float(v_scale), **self._static)
+        if block_table.dtype == torch.int64:
+            params.flags |= self._native.FLAG_TABLE_INT64
         with torch.cuda.device(k.device):
             status = self._lib.pcpa_kv_cache_write(
                 ctypes.byref(params), cfg.interleave_size, int(first_pos), k.shape[1], k.data_ptr(),
@@ -138,3 +143,76 @@ def build_page_pool(config: PCPAttentionConfig, k, v, block_table, *, kv_scale: 
     table = block_table.to(device=k.device, dtype=torch.int32).contiguous()
     KVCacheWriter(cfg)(k, v, pool, table, k_scale=k_scale, v_scale=v_scale, page_valid_len=valid)
     return pool, k_scale, v_scale, valid
+
+
+class PageAllocator:
+    """Free-page stack on the GPU for block tables filled as history grows.
+
+    The reference places every rank's blocks into a padded local cache on
+    the host (run_poc.py:231-237, layout.py:54-98).  Here pages of one pool
+    are handed out on the device: ``allocate(first_pos, num_tokens,
+    block_table)`` gives every cache block that the positions reach and
+    whose table entry is negative a page from the top of the stack, in
+    (rank, block) order, without a host round trip (``pcpa_page_alloc``).
+    ``free_count`` (a 0-d int32 GPU tensor) is the stack height; a block that
+    finds the stack empty keeps its negative entry and its tokens are not
+    written.  Initially pages are handed out in ascending order.
+    """
+
+    def __init__(self, config: PCPAttentionConfig, device, num_pages: Optional[int] = None):
+        import torch
+
+        from .. import _native
+
+        self.config = replace(config, backend="hip").validate()
+        self.num_pages = self.config.num_pages if num_pages is None else int(num_pages)
+        self._native = _native
+        self._lib = _native.load_library()
+        # the top of the stack is the last element: page 0 is handed out first
+        self.free_pages = torch.arange(self.num_pages - 1, -1, -1, dtype=torch.int32, device=device)
+        self.free_count = torch.tensor(self.num_pages, dtype=torch.int32, device=device)
+        self._params = self._native.PcpaParams(
+            abi_version=_native.ABI_VERSION, pcp_size=self.config.pcp_size, num_q_heads=self.config.num_q_heads,
+            num_kv_heads=self.config.num_kv_heads, head_dim=self.config.head_dim,
+            local_q_len=self.config.local_q_len, block_size=self.config.block_size,
+            max_local_blocks=self.config.max_local_blocks, num_pages=self.num_pages, q_dtype=_native.DTYPE_BF16,
+            kv_dtype=_KV_DTYPE_CODES[self.config.kv_dtype], out_dtype=_native.DTYPE_BF16,
+            softmax_scale=self.config.softmax_scale, k_scale=1.0, v_scale=1.0, flags=0)
+
+    def empty_table(self, dtype=None):
+        """A block table with no page assigned (every entry -1)."""
+        import torch
+
+        cfg = self.config
+        return torch.full((cfg.pcp_size, cfg.max_local_blocks), -1, dtype=dtype or torch.int32,
+                          device=self.free_pages.device)
+
+    def allocate(self, first_pos: int, num_tokens: int, block_table) -> None:
+        """Assign pages to the blocks that positions [first_pos, first_pos + num_tokens) reach (asynchronous)."""
+        import torch
+
+        cfg = self.config
+        if (tuple(block_table.shape) != (cfg.pcp_size, cfg.max_local_blocks)
+                or block_table.dtype not in (torch.int32, torch.int64) or not block_table.is_contiguous()
+                or block_table.device != self.free_pages.device):
+            raise ValueError("block_table must be a contiguous int32/int64 tensor "
+                             f"{(cfg.pcp_size, cfg.max_local_blocks)} on {self.free_pages.device}")
+        flags = self._native.FLAG_TABLE_INT64 if block_table.dtype == torch.int64 else 0
+        params = self._native.PcpaParams.from_buffer_copy(self._params)
+        params.flags = flags
+        with torch.cuda.device(block_table.device):
+            status = self._lib.pcpa_page_alloc(
+                ctypes.byref(params), cfg.interleave_size, int(first_pos), int(num_tokens), block_table.data_ptr(),
+                self.free_pages.data_ptr(), self.free_count.data_ptr(),
+                torch.cuda.current_stream(block_table.device).cuda_stream)
+        self._native.check(status)
+
+
+def append_history(writer: KVCacheWriter, allocator: PageAllocator, k, v, kv_pages, block_table, page_valid_len, *,
+                   first_pos: int, k_scale: float = 1.0, v_scale: float = 1.0) -> None:
+    """Append tokens ``first_pos ..`` to a paged history: pages for the blocks
+    they reach (``allocator``), then quantise and write them (``writer``),
+    raising ``page_valid_len``.  Two launches on the current stream."""
+    allocator.allocate(first_pos, k.shape[1], block_table)
+    writer(k, v, kv_pages, block_table, first_pos=first_pos, k_scale=k_scale, v_scale=v_scale,
+           page_valid_len=page_valid_len)

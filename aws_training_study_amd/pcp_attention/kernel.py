@@ -47,10 +47,6 @@ _KV_DTYPE_CODES = {"fp8_e4m3fn": 2, "bfloat16": 1}
 
 PRECISIONS = ("auto", "fp8", "bf16")
 EXP2_MODES = ("fast", "exact")
-# Below this many valid history tokens, ``precision="auto"`` runs an e4m3
-# cache through BF16 MFMAs: e4m3 rounding of Q and P is noise that is only
-# averaged away over many keys (at 785 tokens it reaches a 2e-2 max error).
-AUTO_BF16_BELOW_TOKENS = 2048
 
 
 def _torch_kv_dtype(name: str):
@@ -74,13 +70,22 @@ class HistoryAttentionKernel:
     * ``block_table``: int ``[pcp, max_local_blocks]`` page of each cache block.
     * validity: ``page_valid_len`` (int ``[pcp, max_local_blocks]``), or the
       reference's ``block_valid_mask`` (run_poc.py:137-153, shared by all
-      ranks), or neither, in which case the config's ``actual_history_len``
-      decides.
+      ranks; a GPU mask is converted on the GPU, a CPU mask on the host with
+      its values checked), or neither, in which case the config's
+      ``actual_history_len`` decides.
+    * ``block_table``: int32 or int64 (read as is by the kernels; entries
+      outside ``[0, num_pages)`` are empty pages).
     * ``k_scale``/``v_scale``: per-tensor dequantisation scales of K and V.
     * ``precision``: for an e4m3 cache, ``"fp8"`` runs both GEMMs as e4m3
       MFMAs (Q and P rounded to e4m3), ``"bf16"`` as BF16 MFMAs on the exactly
-      widened cache, and ``"auto"`` picks ``"bf16"`` when the config's
-      ``actual_history_len`` is below ``AUTO_BF16_BELOW_TOKENS``.
+      widened cache, and ``"auto"`` (default) runs e4m3 MFMAs with the
+      precision guard: every row whose probability mass
+      ``sum_k 2^(x_k - m)`` is below ``_native.GUARD_MIN_MASS`` - few valid
+      keys, or a peaked score distribution, where the e4m3 rounding of Q and
+      P is not averaged away - is recomputed on the device with BF16 MFMAs
+      (a second launch whose workgroups exit at once when they hold no such
+      row).  The decision is made per row on the GPU from the runtime
+      lengths and data; nothing is read back to the host.
     * ``exp2``: how the e4m3 MFMA path at head_dim 256 forms the e4m3
       probabilities.  ``"fast"`` (default) writes the e4m3 code of 2^x
       directly, interpolating the exponential linearly between powers of two
@@ -90,11 +95,15 @@ class HistoryAttentionKernel:
 
     * ``splits``: cut the history into this many ranges of table entries run
       by separate workgroups and merged by log-sum-exp; ``"auto"`` splits
-      only when the (row tile, KV head) workgroups would leave CUs idle.
-      The partial results go to ``workspace`` (a uint8 GPU tensor of
-      ``split_workspace_bytes(splits)`` bytes) or, if none is given, to a
-      workspace the kernel object keeps: split calls through one object
-      that may overlap (other streams) need their own.
+      only when the (row tile, KV head) workgroups would leave CUs idle,
+      judged from the runtime history when its lengths are host tensors
+      (``page_valid_len`` or ``block_valid_mask`` on the CPU, or neither
+      given), else from the config's ``actual_history_len``.
+      Split partials and the guard's row flags go to ``workspace`` (a uint8
+      GPU tensor of ``workspace_bytes(splits, precision)`` bytes) or, if
+      none is given, to a workspace the kernel object keeps: split or
+      guarded calls through one object that may overlap (other streams)
+      need their own.
     * ``return_lse``: also return each row's log-sum-exp (float32
       ``[pcp, Hq, local_q]``, natural log of the sum of ``exp(score)`` over
       the valid history keys, ``-inf`` for none) - the input of a merge with
@@ -141,12 +150,12 @@ class HistoryAttentionKernel:
         )
 
     def uses_bf16_mfma(self, precision: str = "auto") -> bool:
-        """Whether a call with ``precision`` runs BF16 MFMAs."""
-        if self.config.kv_dtype != "fp8_e4m3fn" or precision == "bf16":
-            return True
-        if precision == "fp8":
-            return False
-        return self.config.actual_history_len < AUTO_BF16_BELOW_TOKENS
+        """Whether a call with ``precision`` runs its (first) pass on BF16 MFMAs."""
+        return self.config.kv_dtype != "fp8_e4m3fn" or precision == "bf16"
+
+    def guarded(self, precision: str = "auto") -> bool:
+        """Whether a call with ``precision`` runs the precision guard (e4m3 cache, ``"auto"``)."""
+        return self.config.kv_dtype == "fp8_e4m3fn" and precision == "auto"
 
     def default_page_valid_len(self, device) -> Any:
         from .paging import page_valid_lengths
@@ -154,6 +163,30 @@ class HistoryAttentionKernel:
         if self._default_valid is None or self._default_valid.device != device:
             self._default_valid = page_valid_lengths(self.config).to(device)
         return self._default_valid
+
+    def _resolve_lengths(self, device, page_valid_len, block_valid_mask):
+        """(int32 page_valid_len on ``device``, valid tokens if known on the host else None)."""
+        import torch
+
+        from .paging import valid_lengths_from_block_mask
+
+        cfg = self.config
+        table_shape = (cfg.pcp_size, cfg.max_local_blocks)
+        if page_valid_len is not None and block_valid_mask is not None:
+            raise ValueError("pass either page_valid_len or block_valid_mask, not both")
+        if page_valid_len is None and block_valid_mask is None:
+            return self.default_page_valid_len(device), cfg.actual_history_len
+        if page_valid_len is None:
+            # a GPU mask is converted on the GPU (no host round trip)
+            page_valid_len = valid_lengths_from_block_mask(block_valid_mask, cfg)
+        if tuple(page_valid_len.shape) != table_shape:
+            raise ValueError(f"page_valid_len must be {table_shape}, got {tuple(page_valid_len.shape)}")
+        tokens = None
+        if not page_valid_len.is_cuda:
+            tokens = int(page_valid_len.to(torch.int64).clamp(0, cfg.block_size).sum())
+        if page_valid_len.dtype != torch.int32 or page_valid_len.device != device or not page_valid_len.is_contiguous():
+            page_valid_len = page_valid_len.to(device=device, dtype=torch.int32).contiguous()
+        return page_valid_len, tokens
 
     def __call__(
         self,
@@ -206,21 +239,11 @@ class HistoryAttentionKernel:
         table_shape = (cfg.pcp_size, cfg.max_local_blocks)
         if tuple(block_table.shape) != table_shape:
             raise ValueError(f"block_table must be {table_shape}, got {tuple(block_table.shape)}")
-        if block_table.dtype != torch.int32 or block_table.device != device or not block_table.is_contiguous():
+        if (block_table.dtype not in (torch.int32, torch.int64) or block_table.device != device
+                or not block_table.is_contiguous()):
             block_table = block_table.to(device=device, dtype=torch.int32).contiguous()
-        if page_valid_len is not None and block_valid_mask is not None:
-            raise ValueError("pass either page_valid_len or block_valid_mask, not both")
-        if page_valid_len is None:
-            if block_valid_mask is not None:
-                from .paging import valid_lengths_from_block_mask
-
-                page_valid_len = valid_lengths_from_block_mask(block_valid_mask, cfg)
-            else:
-                page_valid_len = self.default_page_valid_len(device)
-        if tuple(page_valid_len.shape) != table_shape:
-            raise ValueError(f"page_valid_len must be {table_shape}, got {tuple(page_valid_len.shape)}")
-        if page_valid_len.dtype != torch.int32 or page_valid_len.device != device or not page_valid_len.is_contiguous():
-            page_valid_len = page_valid_len.to(device=device, dtype=torch.int32).contiguous()
+        table64 = block_table.dtype == torch.int64
+        page_valid_len, tokens = self._resolve_lengths(device, page_valid_len, block_valid_mask)
         if out is None:
             out = torch.empty(q_shape, dtype=torch.bfloat16, device=device)
         elif tuple(out.shape) != q_shape or out.dtype != torch.bfloat16 or not out.is_contiguous() or out.device != device:
@@ -229,7 +252,8 @@ class HistoryAttentionKernel:
         if return_lse:
             lse = torch.empty(q_shape[:3], dtype=torch.float32, device=device)
         bf16_mfma = self.uses_bf16_mfma(precision)
-        key = (num_pages, float(k_scale), float(v_scale), bf16_mfma, exp2)
+        guard = self.guarded(precision)
+        key = (num_pages, float(k_scale), float(v_scale), bf16_mfma, exp2, guard, table64)
         params = self._call_params.get(key)
         if params is None:
             params = self._params(num_pages, k_scale, v_scale)
@@ -237,20 +261,28 @@ class HistoryAttentionKernel:
                 params.flags |= self._native.FLAG_BF16_MFMA
             if exp2 == "exact":
                 params.flags |= self._native.FLAG_EXACT_EXP2
+            if guard:
+                params.flags |= self._native.FLAG_PRECISION_GUARD
+            if table64:
+                params.flags |= self._native.FLAG_TABLE_INT64
             if len(self._call_params) >= 64:
                 self._call_params.clear()
             self._call_params[key] = params
         if splits == "auto":
-            n_split = self._splits.get((device, bf16_mfma))
+            skey = (device, bf16_mfma, tokens)
+            n_split = self._splits.get(skey)
             if n_split is None:
-                n_split = self._splits[(device, bf16_mfma)] = self.split_count(device, bf16_mfma)
+                if len(self._splits) >= 64:
+                    self._splits.clear()
+                n_split = self._splits[skey] = self.split_count(device, bf16_mfma, tokens)
         else:
             n_split = int(splits)
         with torch.cuda.device(device):
             stream = torch.cuda.current_stream(device).cuda_stream
-            if n_split > 1:
+            if n_split > 1 or guard:
+                size = self.workspace_bytes(n_split, precision)
                 if workspace is None:
-                    workspace = self._workspace(params, n_split, device)
+                    workspace = self._workspace(size, device)
                 elif workspace.dtype != torch.uint8 or workspace.device != device or not workspace.is_contiguous():
                     raise ValueError(f"workspace must be a contiguous uint8 tensor on {device}")
                 status = self._lib.pcpa_history_attention_split(
@@ -285,9 +317,10 @@ class HistoryAttentionKernel:
 
         The output buffer (``out=``, allocated here if not given) and the
         log-sum-exp (``return_lse=True``) are fixed; ``replay()`` recomputes
-        them from the current contents of the same input tensors.  A split
-        call gets a workspace of its own, held by the graph, so replays do
-        not share it with eager calls or other graphs.
+        them from the current contents of the same input tensors (a GPU
+        ``block_valid_mask`` is converted to page lengths inside the graph).
+        A split or guarded call gets a workspace of its own, held by the
+        graph, so replays do not share it with eager calls or other graphs.
         """
         import torch
 
@@ -298,18 +331,17 @@ class HistoryAttentionKernel:
         if kwargs.get("workspace") is None:
             kwargs["workspace"] = self.graph_workspace(q.device, kwargs.get("precision", "auto"),
                                                        kwargs.get("splits", "auto"))
-        page_valid_len = kwargs.pop("page_valid_len", None)
-        if page_valid_len is None:
-            if block_valid_mask is not None:
-                from .paging import valid_lengths_from_block_mask
+        # host-side lengths and tables move to the GPU once, outside the graph
+        if block_valid_mask is not None and not block_valid_mask.is_cuda:
+            from .paging import valid_lengths_from_block_mask
 
-                page_valid_len = valid_lengths_from_block_mask(block_valid_mask, self.config)
-            else:
-                page_valid_len = self.default_page_valid_len(q.device)
-        page_valid_len = page_valid_len.to(device=q.device, dtype=torch.int32).contiguous()
-        block_table = block_table.to(device=q.device, dtype=torch.int32).contiguous()
-        return GraphedLaunch(
-            lambda: self(q, kv_pages, block_table, page_valid_len=page_valid_len, **kwargs), warmup=warmup)
+            kwargs["page_valid_len"] = valid_lengths_from_block_mask(block_valid_mask, self.config)
+            block_valid_mask = None
+        if kwargs.get("page_valid_len") is not None:
+            kwargs["page_valid_len"] = kwargs["page_valid_len"].to(device=q.device, dtype=torch.int32).contiguous()
+        if not block_table.is_cuda or block_table.dtype not in (torch.int32, torch.int64):
+            block_table = block_table.to(device=q.device, dtype=torch.int32).contiguous()
+        return GraphedLaunch(lambda: self(q, kv_pages, block_table, block_valid_mask, **kwargs), warmup=warmup)
 
     # Query rows per workgroup and workgroups per CU: the e4m3 head_dim-256
     # kernel takes 256 rows and a whole CU; the tile kernel 128 rows, two
@@ -319,17 +351,18 @@ class HistoryAttentionKernel:
     # the MI355X: the overlap kernel's deeper pipeline needs longer ranges).
     MIN_TILES_PER_SPLIT = {"overlap": 16, "tile": 4}
 
-    def split_count(self, device, bf16_mfma: bool) -> int:
+    def split_count(self, device, bf16_mfma: bool, tokens=None) -> int:
         """History splits for ``splits="auto"`` on ``device`` (``auto_splits``)."""
         import torch
 
-        return self.auto_splits(bf16_mfma, torch.cuda.get_device_properties(device).multi_processor_count)
+        return self.auto_splits(bf16_mfma, torch.cuda.get_device_properties(device).multi_processor_count, tokens)
 
-    def auto_splits(self, bf16_mfma: bool, cus: int) -> int:
+    def auto_splits(self, bf16_mfma: bool, cus: int, tokens=None) -> int:
         """Enough (row tile, KV head, split) workgroups to fill the workgroup
         slots of ``cus`` CUs, each split still walking ``MIN_TILES_PER_SPLIT``
-        tiles and holding a table entry; 1 when the row tiles already fill
-        the GPU."""
+        tiles of the ``tokens`` valid history tokens (default: the config's
+        ``actual_history_len``) and holding a table entry; 1 when the row
+        tiles already fill the GPU."""
         cfg = self.config
         overlap = not bf16_mfma and cfg.kv_dtype == "fp8_e4m3fn" and cfg.head_dim == 256
         kind = "overlap" if overlap else "tile"
@@ -339,35 +372,41 @@ class HistoryAttentionKernel:
         slots = cus * per_cu
         if items >= slots:
             return 1
-        tiles = -(-cfg.actual_history_len // 64)
+        tiles = -(-(cfg.actual_history_len if tokens is None else tokens) // 64)
         entries = cfg.pcp_size * cfg.max_local_blocks
         return max(1, min(self._native.MAX_SPLITS, entries, -(-slots // items),
                           tiles // self.MIN_TILES_PER_SPLIT[kind]))
 
-    def split_workspace_bytes(self, n_split: int) -> int:
-        """Bytes of the workspace of a call with ``n_split`` splits."""
-        size = self._lib.pcpa_split_workspace_bytes(ctypes.byref(self._params(self.config.num_pages, 1.0, 1.0)),
-                                                    n_split)
+    def workspace_bytes(self, n_split: int, precision: str = "auto") -> int:
+        """Bytes of the workspace of a call with ``n_split`` splits and ``precision``."""
+        params = self._params(self.config.num_pages, 1.0, 1.0)
+        if self.guarded(precision):
+            params.flags |= self._native.FLAG_PRECISION_GUARD
+        size = self._lib.pcpa_split_workspace_bytes(ctypes.byref(params), n_split)
         if size < 0:
             self._native.check(int(size))
         return int(size)
 
+    def split_workspace_bytes(self, n_split: int) -> int:
+        """Bytes of the split partials of a call with ``n_split`` splits (no guard)."""
+        return self.workspace_bytes(n_split, precision="fp8")
+
     def graph_workspace(self, device, precision="auto", splits="auto"):
-        """A new workspace for a call that ``precision``/``splits`` would split, else ``None``."""
+        """A new workspace for a call that ``precision``/``splits`` would split or guard, else ``None``."""
         import torch
 
         n_split = self.split_count(device, self.uses_bf16_mfma(precision)) if splits == "auto" else int(splits)
-        if n_split <= 1:
+        size = self.workspace_bytes(n_split, precision)
+        if size <= 0:
             return None
-        return torch.empty(self.split_workspace_bytes(n_split), dtype=torch.uint8, device=device)
+        return torch.empty(size, dtype=torch.uint8, device=device)
 
-    def _workspace(self, params, n_split: int, device):
+    def _workspace(self, size: int, device):
         import torch
 
-        size = self.split_workspace_bytes(n_split)
         ws = getattr(self, "_split_ws", None)
         if ws is None or ws.device != device or ws.numel() < size:
-            ws = torch.empty(size, dtype=torch.uint8, device=device)
+            ws = torch.empty(max(size, 16), dtype=torch.uint8, device=device)
             self._split_ws = ws
         return ws
 

@@ -71,11 +71,19 @@ def valid_lengths_from_block_mask(mask: torch.Tensor, config: PCPAttentionConfig
     valid key and ``-9984`` for a padded one (run_poc.py:137-153); it applies
     to every rank.  Only prefix masks of those two values are representable,
     which is every mask the reference builds.
+
+    A CPU mask is converted on the host and its values are checked
+    (``ValueError`` otherwise).  A GPU mask is converted by a HIP kernel on
+    the current stream, with no host synchronisation (so the call can be
+    captured in a HIP graph): each block's length is the number of leading
+    keys with a zero bias, and the values are not checked.
     """
     kv_tiles = config.block_size // 128
     expected = (config.max_local_blocks, kv_tiles, 1, 128)
     if config.block_size % 128 or tuple(mask.shape) != expected:
         raise ValueError(f"expected block_valid_mask shape {expected}, got {tuple(mask.shape)}")
+    if mask.is_cuda:
+        return _device_valid_lengths(mask, config)
     bias = mask.detach().to("cpu", torch.float32).reshape(config.max_local_blocks, config.block_size)
     valid = bias == 0
     if not bool(torch.all(valid | (bias <= MASKED_SCORE_BIAS))):
@@ -85,6 +93,22 @@ def valid_lengths_from_block_mask(mask: torch.Tensor, config: PCPAttentionConfig
     if not bool(torch.all(prefix == valid)):
         raise ValueError("block_valid_mask must mark a prefix of every cache block as valid")
     return counts.to(torch.int32)[None, :].expand(config.pcp_size, -1).contiguous()
+
+
+def _device_valid_lengths(mask: torch.Tensor, config: PCPAttentionConfig) -> torch.Tensor:
+    from .. import _native
+
+    if mask.dtype != torch.bfloat16:
+        raise ValueError(f"a GPU block_valid_mask must be bfloat16, got {mask.dtype}")
+    mask = mask.contiguous()
+    lengths = torch.empty((config.pcp_size, config.max_local_blocks), dtype=torch.int32, device=mask.device)
+    lib = _native.load_library()
+    with torch.cuda.device(mask.device):
+        status = lib.pcpa_block_mask_valid_len(mask.data_ptr(), config.pcp_size, config.max_local_blocks,
+                                               config.block_size, lengths.data_ptr(),
+                                               torch.cuda.current_stream(mask.device).cuda_stream)
+    _native.check(status)
+    return lengths
 
 
 def pack_page_pool(

@@ -51,6 +51,11 @@ def parse_args(argv=None):
                              "of the current tokens merged with the history output; launch: per-call latency of "
                              "the workload's history attention, eager calls against a replayed HIP graph")
     parser.add_argument("--seed", type=int, default=1234)
+    parser.add_argument("--precision", choices=("auto", "fp8", "bf16"), default="auto",
+                        help="MFMA precision of an e4m3 cache: auto (e4m3 MFMAs with the precision guard that "
+                             "recomputes low-mass rows with BF16 MFMAs), fp8 (e4m3 only) or bf16")
+    parser.add_argument("--exp2", choices=("fast", "exact"), default="fast",
+                        help="e4m3 probabilities at head_dim 256: linear-mantissa exp2 (fast) or v_exp_f32 (exact)")
     parser.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
                         help="approximate CPU time budget of the ring-model baseline sample")
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -458,7 +463,7 @@ def main(argv=None) -> int:
 
     def step():
         kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len,
-               k_scale=problem.k_scale, v_scale=problem.v_scale, out=out)
+               k_scale=problem.k_scale, v_scale=problem.v_scale, out=out, precision=args.precision, exp2=args.exp2)
 
     for _ in range(args.warmup):
         step()
@@ -470,7 +475,7 @@ def main(argv=None) -> int:
 
     flops = model_flops(cfg)
     ms_per_step = wall_s * 1e3 / args.steps
-    fp8 = not kernel.uses_bf16_mfma()
+    fp8 = not kernel.uses_bf16_mfma(args.precision)
     peak = PEAK_TFLOPS["fp8_e4m3fn" if fp8 else "bfloat16"]
     achieved = flops / (kernel_ms * 1e-3) / 1e12
     traffic, traffic_source = (args.traffic_bytes, "--traffic-bytes") if args.traffic_bytes else \
@@ -503,6 +508,11 @@ def main(argv=None) -> int:
             "block_size": cfg.block_size,
             "interleave": cfg.interleave_size,
             "kv_dtype": cfg.kv_dtype,
+            "mfma": "e4m3" if fp8 else "bf16",
+            "exp2": (args.exp2 + (" (linear-mantissa e4m3 code)" if args.exp2 == "fast" else " (v_exp_f32)"))
+            if fp8 and cfg.head_dim == 256 else "exact (v_exp_f32)",
+            "precision_guard": kernel.guarded(args.precision),
+            "splits": kernel.split_count(device, not fp8),
         },
         "pct_peak": round(100.0 * flops / (ms_per_step * 1e-3) / 1e12 / peak, 2),
         "kernel_ms": _kernel_ms(kernel_ms, spread),

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define PCPA_ABI_VERSION 1
+#define PCPA_ABI_VERSION 2
 
 /* Status codes. */
 #define PCPA_OK 0
@@ -40,6 +40,7 @@ extern "C" {
 #define PCPA_ERR_LAUNCH (-7)        /* the HIP launch itself failed          */
 #define PCPA_ERR_TOO_LARGE (-8)     /* an index would overflow 32/64-bit maths */
 #define PCPA_ERR_BAD_SCALE (-9)     /* a scale is not finite and positive    */
+#define PCPA_ERR_WORKSPACE (-10)    /* workspace missing or too small        */
 
 /* params.flags bits. */
 /* Run both GEMMs as BF16 MFMAs even for an e4m3 cache: K/V are widened to
@@ -53,6 +54,27 @@ extern "C" {
  * the exponential between powers of two first).  Slower; ignored elsewhere,
  * where P always comes from v_exp_f32. */
 #define PCPA_FLAG_EXACT_EXP2 2u
+/* Precision guard for e4m3 MFMAs (ignored when the launch runs BF16 MFMAs).
+ * e4m3 Q and P carry ~3.6% relative rounding noise per element, which
+ * averages away only when many keys share a row's softmax.  With this flag
+ * the e4m3 pass also measures each row's probability mass
+ *     W = sum_k 2^(x_k - m)        (x_k the score in log2 units, m the
+ *                                    running reference, at most 2.5 below
+ *                                    the row's largest x_k)
+ * and a second launch recomputes, with BF16 MFMAs on the exactly widened
+ * cache (bf16 Q and P), every workgroup holding a row with
+ * W < PCPA_GUARD_MIN_MASS: short histories and peaked score distributions.
+ * The second launch's workgroups exit at once when none of their rows is
+ * flagged.  Needs a workspace of pcpa_split_workspace_bytes bytes (one byte
+ * per query row for the flags), so it is accepted by
+ * pcpa_history_attention_split only (any splits); the other entry points
+ * return PCPA_ERR_WORKSPACE. */
+#define PCPA_FLAG_PRECISION_GUARD 4u
+#define PCPA_GUARD_MIN_MASS 384.0f
+/* block_table holds int64 entries (torch's default integer type) instead of
+ * int32; an entry outside [0, num_pages) is an empty page either way.  Also
+ * accepted by pcpa_kv_cache_write. */
+#define PCPA_FLAG_TABLE_INT64 8u
 
 /* dtype codes. */
 #define PCPA_DTYPE_BF16 1
@@ -64,9 +86,10 @@ extern "C" {
  *   kv_pages     [num_pages, 2, num_kv_heads, block_size, head_dim] kv_dtype
  *                (each row is pack_local_kv's payload, kernel.py:17-29:
  *                 all K of a block, then all V)
- *   block_table  [pcp_size, max_local_blocks] int32: physical page of
- *                (rank, local block); entries outside [0, num_pages) are
- *                treated as empty pages (never read)
+ *   block_table  [pcp_size, max_local_blocks] int32 (int64 with
+ *                PCPA_FLAG_TABLE_INT64): physical page of (rank, local
+ *                block); entries outside [0, num_pages) are treated as empty
+ *                pages (never read)
  *   page_valid_len [pcp_size, max_local_blocks] int32: number of valid
  *                leading tokens of that cache block, clamped to
  *                [0, block_size].  Valid tokens of a striped rank always
@@ -117,7 +140,7 @@ int32_t pcpa_check_params(const pcpa_params* params);
  * (the reference kernel allocated it, kernel.py:124).
  */
 int32_t pcpa_history_attention(const pcpa_params* params, const void* q, const void* kv_pages,
-                               const int32_t* block_table, const int32_t* page_valid_len,
+                               const void* block_table, const int32_t* page_valid_len,
                                void* out, void* stream);
 
 /*
@@ -133,29 +156,35 @@ int32_t pcpa_history_attention(const pcpa_params* params, const void* q, const v
  * output only (kernel.py:546-551).
  */
 int32_t pcpa_history_attention_lse(const pcpa_params* params, const void* q, const void* kv_pages,
-                                   const int32_t* block_table, const int32_t* page_valid_len,
+                                   const void* block_table, const int32_t* page_valid_len,
                                    void* out, float* lse, void* stream);
 
 /*
- * Split history for workloads with few query rows: the table entries are cut
+ * History attention with a caller-provided workspace: split history and the
+ * precision guard.
+ * Split history, for workloads with few query rows: the table entries are cut
  * into `splits` equal ranges, each (row tile, range) pair runs as its own
- * workgroup and writes a normalised FP32 partial output and log-sum-exp into
- * `workspace`, and a second launch merges the partials by log-sum-exp into
- * `out` (and `lse`, optional).  Results equal pcpa_history_attention_lse's to
- * rounding.  For a launch whose (row tile, KV head) workgroups would leave
- * CUs idle (256 rows and a CU per workgroup for e4m3 MFMAs at head_dim 256,
- * else 128 rows, two per CU).  Every cache dtype, precision and head dim of
- * pcpa_history_attention_lse; splits in [1, PCPA_MAX_SPLITS]
- * (1 = pcpa_history_attention_lse).  workspace: device memory of at least
- * pcpa_split_workspace_bytes(params, splits) bytes, 16-byte aligned; its
- * contents need no initialisation and are left undefined.  The library does
- * not allocate it.  No reference counterpart (the reference's device ring
- * has no split).
+ * workgroup and writes a normalised FP32 partial output, log-sum-exp and
+ * reference maximum into `workspace`, and a second launch merges the
+ * partials by log-sum-exp into `out` (and `lse`, optional).  Results equal
+ * pcpa_history_attention_lse's to rounding.  For a launch whose (row tile,
+ * KV head) workgroups would leave CUs idle (256 rows and a CU per workgroup
+ * for e4m3 MFMAs at head_dim 256, else 128 rows, two per CU).  Every cache
+ * dtype, precision and head dim of pcpa_history_attention_lse; splits in
+ * [1, PCPA_MAX_SPLITS] (1 = one pass).
+ * With PCPA_FLAG_PRECISION_GUARD the workspace also holds the guard's row
+ * flags, and the BF16 pass follows the e4m3 one (or the merge).
+ * workspace: device memory of at least pcpa_split_workspace_bytes(params,
+ * splits) bytes (0 for splits = 1 without the guard, when NULL is
+ * accepted), 16-byte aligned; its contents need no initialisation and are
+ * left undefined.  The library does not allocate it.  No reference
+ * counterpart (the reference's device ring has no split, and its NKI kernel
+ * one precision, kernel.py:84-554).
  */
 #define PCPA_MAX_SPLITS 64
 int64_t pcpa_split_workspace_bytes(const pcpa_params* params, int32_t splits);
 int32_t pcpa_history_attention_split(const pcpa_params* params, int32_t splits, const void* q,
-                                     const void* kv_pages, const int32_t* block_table,
+                                     const void* kv_pages, const void* block_table,
                                      const int32_t* page_valid_len, void* out, float* lse,
                                      void* workspace, int64_t workspace_bytes, void* stream);
 
@@ -210,15 +239,53 @@ int32_t pcpa_current_attention(const pcpa_params* params, int32_t interleave, co
  */
 int32_t pcpa_kv_cache_write(const pcpa_params* params, int32_t interleave, int64_t first_pos,
                             int32_t num_tokens, const void* k, const void* v,
-                            const int32_t* block_table, void* kv_pages, int32_t* page_valid_len,
+                            const void* block_table, void* kv_pages, int32_t* page_valid_len,
                             void* stream);
 
 /*
  * max |x| over n bf16 values into *amax (device float): the amax of the
  * per-tensor e4m3 scale amax / 448 (the FP8 configurations' K/V
- * quantisation).  Two launches on `stream`; *amax needs no initialisation.
+ * quantisation).  A NaN anywhere in x makes *amax NaN, as torch's
+ * x.abs().max() does.  Two launches on `stream`; *amax needs no
+ * initialisation.
  */
 int32_t pcpa_absmax_bf16(const void* x, int64_t n, float* amax, void* stream);
+
+/*
+ * The reference's runtime mask turned into per-page valid lengths on the GPU
+ * (no host round trip, so a mask-form call can be captured in a HIP graph).
+ *   mask  [max_local_blocks, block_size / 128, 1, 128] bf16, the additive
+ *         score bias of make_block_valid_mask (run_poc.py:137-153) that the
+ *         NKI kernel takes as block_valid_mask_ref (kernel.py:113-118,
+ *         341-358): 0 for a valid key, -9984 for padding, shared by all ranks
+ *   page_valid_len [pcp_size, max_local_blocks] int32 (written): for every
+ *         rank, the number of leading keys of the block whose bias is zero.
+ * The reference's masks are always such prefixes; this kernel does not check
+ * that (a host-side conversion can).  block_size must be a multiple of 128.
+ */
+int32_t pcpa_block_mask_valid_len(const void* mask, int32_t pcp_size, int32_t max_local_blocks,
+                                  int32_t block_size, int32_t* page_valid_len, void* stream);
+
+/*
+ * Page allocation for appended history tokens, on the GPU: every cache block
+ * (rank, local block) that the positions [first_pos, first_pos + num_tokens)
+ * reach and whose block_table entry is negative (no page yet) takes a page
+ * from the top of a device free-page stack, in (rank, block) entry order:
+ *   free_pages  int32 stack of free page indices; entries [0, *free_count)
+ *               are free, the top one is free_pages[*free_count - 1]
+ *   free_count  device int32, lowered by the pages taken (not below 0;
+ *               entries that find the stack empty stay negative, and
+ *               pcpa_kv_cache_write then skips their tokens)
+ *   block_table int32 (int64 with PCPA_FLAG_TABLE_INT64), updated in place.
+ * One workgroup; deterministic (the same appends give the same table).  Call
+ * it before pcpa_kv_cache_write for the same positions.  Replaces the
+ * reference's host-side placement of every rank's blocks into its padded
+ * local cache (run_poc.py:231-237, layout.py:54-98); its pages are what
+ * pack_local_kv rows occupy (kernel.py:17-29).  The positions must fit the
+ * cache as for pcpa_kv_cache_write (PCPA_ERR_BAD_SHAPE otherwise).
+ */
+int32_t pcpa_page_alloc(const pcpa_params* params, int32_t interleave, int64_t first_pos, int32_t num_tokens,
+                        void* block_table, const int32_t* free_pages, int32_t* free_count, void* stream);
 
 #ifdef __cplusplus
 }

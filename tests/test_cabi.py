@@ -57,7 +57,7 @@ def test_params_struct_layout():
 
 
 def _good_params(**kw):
-    p = dict(abi_version=1, pcp_size=4, num_q_heads=8, num_kv_heads=2, head_dim=64, local_q_len=64,
+    p = dict(abi_version=_native.ABI_VERSION, pcp_size=4, num_q_heads=8, num_kv_heads=2, head_dim=64, local_q_len=64,
              block_size=128, max_local_blocks=4, num_pages=16, q_dtype=1, kv_dtype=1, out_dtype=1,
              softmax_scale=0.125, k_scale=1.0, v_scale=1.0, flags=0)
     p.update(kw)
@@ -68,13 +68,16 @@ def _good_params(**kw):
     "change,status",
     [
         ({}, 0),
-        ({"abi_version": 2}, -2),
+        ({"abi_version": _native.ABI_VERSION - 1}, -2),
         ({"pcp_size": 0}, -3),
         ({"num_q_heads": 7}, -3),
         ({"flags": 1}, 0),
         ({"flags": 2}, 0),
         ({"flags": 3}, 0),
-        ({"flags": 4}, -3),
+        ({"flags": 4}, 0),
+        ({"flags": 8}, 0),
+        ({"flags": 15}, 0),
+        ({"flags": 16}, -3),
         ({"q_dtype": 2}, -4),
         ({"kv_dtype": 9}, -4),
         ({"head_dim": 96}, -5),
@@ -115,7 +118,13 @@ def test_split_workspace_size_from_python():
                              backend="hip")
     kernel = make_history_attention_kernel(cfg)
     rows = cfg.pcp_size * cfg.num_q_heads * cfg.local_q_len
-    assert kernel.split_workspace_bytes(3) == 3 * rows * (cfg.head_dim + 1) * 4
+    # FP32 partial output, log-sum-exp and reference max per row and split
+    assert kernel.split_workspace_bytes(3) == 3 * rows * (cfg.head_dim + 2) * 4
+    assert kernel.workspace_bytes(1, precision="fp8") == 0
+    # the precision guard needs its flags, plan and fixup partials even for one pass
+    guard = kernel.workspace_bytes(1, precision="auto")
+    assert guard >= rows + 4 * (4 + rows // 128)
+    assert kernel.workspace_bytes(3, precision="auto") >= kernel.split_workspace_bytes(3) + guard
     with pytest.raises(_native.PcpaError, match="BAD_SHAPE"):
         kernel.split_workspace_bytes(_native.MAX_SPLITS + 1)
 
@@ -185,18 +194,50 @@ def test_split_entry_validates_without_a_gpu(lib):
     """pcpa_split_workspace_bytes / pcpa_history_attention_split errors come back before any HIP call."""
     p = _good_params(kv_dtype=2, head_dim=256)  # 4 ranks x 8 heads x 64 tokens = 2048 rows
     size = lib.pcpa_split_workspace_bytes(ctypes.byref(p), 3)
-    assert size == 3 * 2048 * (256 + 1) * 4
+    assert size == 3 * 2048 * (256 + 2) * 4
+    assert lib.pcpa_split_workspace_bytes(ctypes.byref(p), 1) == 0
     assert lib.pcpa_split_workspace_bytes(ctypes.byref(p), 0) == -3
     assert lib.pcpa_split_workspace_bytes(ctypes.byref(p), 65) == -3
-    assert lib.pcpa_split_workspace_bytes(ctypes.byref(_good_params(abi_version=2)), 2) == -2
+    assert lib.pcpa_split_workspace_bytes(ctypes.byref(_good_params(abi_version=1)), 2) == -2
     size = lib.pcpa_split_workspace_bytes(ctypes.byref(p), 2)
     f = lib.pcpa_history_attention_split
-    assert f(ctypes.byref(p), 2, 16, 16, 16, 16, 16, None, None, size, None) == -1          # workspace
-    assert f(ctypes.byref(p), 2, 16, 16, 16, 16, 16, None, 16, size - 16, None) == -3       # too small
+    assert f(ctypes.byref(p), 2, 16, 16, 16, 16, 16, None, None, size, None) == -10         # workspace
+    assert f(ctypes.byref(p), 2, 16, 16, 16, 16, 16, None, 16, size - 16, None) == -10      # too small
     assert f(ctypes.byref(p), 2, 16, 16, 16, 16, 16, None, 8, size, None) == -6             # alignment
     assert f(ctypes.byref(p), 2, 16, 16, 16, 16, 16, 2, 16, size, None) == -6               # lse alignment
     # BF16 caches and BF16 MFMAs split too (tile kernel): their sizes are checked the same way
     for other in (_good_params(head_dim=128), _good_params(kv_dtype=2, head_dim=256, flags=1)):
         need = lib.pcpa_split_workspace_bytes(ctypes.byref(other), 4)
-        assert need == 4 * 2048 * (other.head_dim + 1) * 4
-        assert f(ctypes.byref(other), 4, 16, 16, 16, 16, 16, None, 16, need - 16, None) == -3
+        assert need == 4 * 2048 * (other.head_dim + 2) * 4
+        assert f(ctypes.byref(other), 4, 16, 16, 16, 16, 16, None, 16, need - 16, None) == -10
+    # the guard: no workspace through the entry points that take none
+    g = _good_params(kv_dtype=2, head_dim=256, flags=4)
+    assert lib.pcpa_split_workspace_bytes(ctypes.byref(g), 1) > 0
+    assert lib.pcpa_history_attention(ctypes.byref(g), 16, 16, 16, 16, 16, None) == -10
+    assert f(ctypes.byref(g), 1, 16, 16, 16, 16, 16, None, None, 0, None) == -10
+    # an int64 block table must be 8-byte aligned
+    t = _good_params(flags=8)
+    assert lib.pcpa_history_attention(ctypes.byref(t), 16, 16, 20, 16, 16, None) == -6
+
+
+def test_paging_entries_validate_without_a_gpu(lib):
+    """pcpa_block_mask_valid_len / pcpa_page_alloc errors come back before any HIP call."""
+    m = lib.pcpa_block_mask_valid_len
+    assert m(None, 4, 4, 128, 16, None) == -1
+    assert m(16, 4, 4, 128, None, None) == -1
+    assert m(16, 0, 4, 128, 16, None) == -3
+    assert m(16, 4, 4, 64, 16, None) == -3      # the mask form needs 128-key tiles
+    assert m(17, 4, 4, 128, 16, None) == -6
+    assert m(16, 4, 4, 128, 18, None) == -6
+    a = lib.pcpa_page_alloc
+    p = _good_params()  # 4 ranks x 4 blocks x 128 slots: positions [0, 2048)
+    assert a(None, 16, 0, 8, 16, 16, 16, None) == -1
+    assert a(ctypes.byref(p), 16, 0, 8, None, 16, 16, None) == -1
+    assert a(ctypes.byref(p), 16, 0, 8, 16, None, 16, None) == -1
+    assert a(ctypes.byref(p), 16, 0, 8, 16, 16, None, None) == -1
+    assert a(ctypes.byref(p), 0, 0, 8, 16, 16, 16, None) == -3
+    assert a(ctypes.byref(p), 16, -1, 8, 16, 16, 16, None) == -3
+    assert a(ctypes.byref(p), 16, 0, 8, 18, 16, 16, None) == -6
+    assert a(ctypes.byref(_good_params(flags=8)), 16, 0, 8, 20, 16, 16, None) == -6
+    assert a(ctypes.byref(p), 16, 2040, 9, 16, 16, 16, None) == -3   # past the cache's capacity
+    assert a(ctypes.byref(p), 16, 0, 0, 16, 16, 16, None) == 0       # nothing to place

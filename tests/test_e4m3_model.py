@@ -1,0 +1,195 @@
+"""Pins of the e4m3 numerical model (oracle/e4m3_model.py) on the CPU.
+
+The model is the yardstick for the e4m3-MFMA kernels' own rounding error, so
+it is pinned independently of them: with its two roundings switched off it
+is the float64 attention of the oracle; a scalar per-row loop written here
+from the kernels' description gives the same numbers; closed forms hold
+(identical keys, one dominant key, the linear-mantissa code); and its e4m3
+rounding agrees with torch's float8_e4m3fn cast.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from aws_training_study_amd.pcp_attention.config import PCPAttentionConfig
+from aws_training_study_amd.pcp_attention.workloads import build_paged_problem
+from oracle import e4m3_model as em
+from oracle import pcp_oracle as orc
+
+
+def _problem(seed=3, **kw):
+    base = dict(pcp_size=2, current_len=128, max_history_len=1024, actual_history_len=1000, block_size=128,
+                interleave_size=32, num_q_heads=4, num_kv_heads=2, head_dim=64, backend="hip")
+    base.update(kw)
+    cfg = PCPAttentionConfig(**base).validate()
+    return cfg, build_paged_problem(cfg, seed, kv_scale="per_tensor")
+
+
+def _inputs(problem):
+    qbits = problem.q_stacked.view(torch.int16).numpy().view(np.uint16)
+    pool = problem.kv_pages.view(torch.uint8).numpy()
+    return qbits, pool, problem.block_table.numpy(), problem.page_valid_len.numpy()
+
+
+def _model(cfg, problem, **kw):
+    qbits, pool, table, lens = _inputs(problem)
+    return em.emulate_rows(qbits, pool, table, lens, num_kv_heads=cfg.num_kv_heads, block_size=cfg.block_size,
+                           softmax_scale=cfg.softmax_scale, k_scale=problem.k_scale, v_scale=problem.v_scale, **kw)
+
+
+def test_round_e4m3_matches_torch_cast():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(20000) * np.exp2(rng.integers(-12, 9, 20000)),
+                        [0.0, -0.0, 448.0, 448.01, -463.9, 2.0 ** -9, 2.0 ** -10, 3 * 2.0 ** -10, 1.0625, 1.1875]])
+    x = x[np.abs(x) < 464].astype(np.float32)
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).float().numpy().astype(np.float64)
+    np.testing.assert_array_equal(em.round_e4m3(x), want)
+
+
+def test_fast_code_is_the_linear_interpolation_of_exp2():
+    x = np.linspace(-7.0, 8.4, 4001)
+    codes = em.fast_exp2_code(x)
+    got = orc.decode_e4m3fn(codes)
+    n = np.floor(x)
+    linear = np.exp2(n) * (1 + (x - n))
+    # the code is the linear form rounded to e4m3's 3 mantissa bits (normal range)
+    normal = x >= -6
+    np.testing.assert_allclose(got[normal], em.round_e4m3(linear[normal]), rtol=0, atol=0)
+    assert np.all(np.abs(got[normal] / np.exp2(x[normal]) - 1) <= 0.125)
+
+
+@pytest.mark.parametrize("kernel,head_dim", [("overlap", 256), ("tile", 64), ("tile", 128)])
+def test_without_rounding_it_is_float64_attention(kernel, head_dim):
+    cfg, problem = _problem(head_dim=head_dim)
+    out, lse = _model(cfg, problem, kernel=kernel, q_round=False, p_round=False)
+    qbits, pool, table, lens = _inputs(problem)
+    shape = orc.OracleShape.from_config(cfg)
+    want = orc.paged_history_attention(orc.decode_bfloat16(qbits), orc.decode_e4m3fn(pool), table, lens, shape,
+                                       problem.k_scale, problem.v_scale)
+    # (scores are rounded to fp32, as the MFMAs accumulate them)
+    np.testing.assert_allclose(out, want, rtol=0, atol=2e-6)
+    # the log-sum-exp against a direct sum over the same keys
+    q = orc.decode_bfloat16(qbits)[0, 0, 0]
+    k = orc.decode_e4m3fn(pool).reshape(-1, 2, cfg.num_kv_heads, cfg.block_size, head_dim)
+    keys = np.concatenate([k[table[r, b], 0, 0, :lens[r, b]] for r in range(cfg.pcp_size)
+                           for b in range(cfg.max_local_blocks) if lens[r, b] > 0]) * problem.k_scale
+    direct = math.log(math.fsum(np.exp(keys @ q * cfg.softmax_scale)))
+    assert abs(lse[0, 0, 0] - direct) < 1e-5
+
+
+def _scalar_row(q_bits_row, keys, vals, tiles, c_factor, kernel, exp2):
+    """One row of the overlap kernel's arithmetic written as a plain loop."""
+    q = orc.decode_bfloat16(q_bits_row).astype(np.float32)
+    amax = np.float32(np.abs(q).max())
+    inv = np.float32(448.0) / amax
+    sigma = amax / np.float32(448.0)
+    q8 = np.array([em.round_e4m3(np.float32(x * inv)) for x in q])
+    c = np.float32(sigma * c_factor)
+    m = np.float32(-1.0e30)
+    o = np.zeros(vals.shape[1])
+    l = 0.0
+    key = 0
+    for n in tiles:
+        s = [np.float32(float(np.dot(q8, keys[key + i]))) for i in range(n)]
+        mxs = np.float32(np.float32(max(s)) * c)
+        m_new = max(m, np.float32(mxs - np.float32(2.5)))
+        alpha = 2.0 ** float(np.float32(m - m_new))
+        m = m_new
+        o *= alpha
+        l *= alpha
+        for i in range(n):
+            if exp2 == "fast":
+                y = np.float32(float(s[i]) * float(np.float32(8) * c) + float(np.float32(-8.0 * float(m) + 104.0)))
+                p = float(orc.decode_e4m3fn(np.uint8(min(255, max(0, int(np.rint(float(y))))))))
+            else:
+                x = np.float32(float(s[i]) * float(c) + float(np.float32(6.0 - float(m))))
+                p = float(em.round_e4m3(np.float32(2.0 ** float(x))))
+            o += p * vals[key + i]
+            l += p
+        key += n
+    return o / l
+
+
+@pytest.mark.parametrize("exp2", ["fast", "exact"])
+def test_vectorised_model_equals_a_scalar_loop(exp2):
+    cfg, problem = _problem(head_dim=256, actual_history_len=777, seed=9)
+    rows = np.array([[0, 0, 0], [1, 3, 63], [0, 2, 17]])
+    out, _ = _model(cfg, problem, kernel="overlap", exp2=exp2, rows=rows)
+    qbits, pool, table, lens = _inputs(problem)
+    walk = em.walk_pages(table, lens, pool.shape[0], cfg.block_size)
+    tiles = em._tiles(walk)
+    dec = orc.decode_e4m3fn(pool).reshape(-1, 2, cfg.num_kv_heads, cfg.block_size, cfg.head_dim)
+    c_factor = np.float32(np.float32(np.float32(cfg.softmax_scale) * np.float32(problem.k_scale)) * em.LOG2E)
+    group = cfg.num_q_heads // cfg.num_kv_heads
+    for i, (rank, qh, tok) in enumerate(rows):
+        g = qh // group
+        keys = np.concatenate([dec[p, 0, g, b:b + n] for p, b, n in tiles])
+        vals = np.concatenate([dec[p, 1, g, b:b + n] for p, b, n in tiles])
+        want = _scalar_row(qbits[rank, qh, tok], keys, vals, [n for _, _, n in tiles], c_factor, "overlap", exp2)
+        np.testing.assert_allclose(out[i], want * problem.v_scale, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("kernel,exp2", [("overlap", "fast"), ("overlap", "exact"), ("tile", "exact")])
+def test_identical_keys_give_the_mean_of_v(kernel, exp2):
+    """Equal scores give equal probabilities whatever their rounding: O = mean(V)."""
+    cfg, problem = _problem(head_dim=256 if kernel == "overlap" else 128, actual_history_len=1024)
+    pool = problem.kv_pages.view(torch.uint8).numpy().copy().reshape(-1, 2, cfg.num_kv_heads, cfg.block_size,
+                                                                     cfg.head_dim)
+    pool[:, 0] = pool[0, 0, :, :1]  # every key of every page equals one key
+    qbits, _, table, lens = _inputs(problem)
+    out, _ = em.emulate_rows(qbits, pool.reshape(pool.shape[0], -1), table, lens, num_kv_heads=cfg.num_kv_heads,
+                             block_size=cfg.block_size, softmax_scale=cfg.softmax_scale, k_scale=problem.k_scale,
+                             v_scale=problem.v_scale, kernel=kernel, exp2=exp2)
+    dec = orc.decode_e4m3fn(pool)
+    mean_v = np.stack([np.concatenate([dec[table[r, b], 1, g, :lens[r, b]] for r in range(cfg.pcp_size)
+                                       for b in range(cfg.max_local_blocks)]).mean(0) for g in range(2)])
+    group = cfg.num_q_heads // cfg.num_kv_heads
+    want = np.stack([mean_v[h // group] for h in range(cfg.num_q_heads)])[None, :, None, :] * problem.v_scale
+    np.testing.assert_allclose(out, np.broadcast_to(want, out.shape), rtol=1e-12, atol=1e-12)
+
+
+def test_a_dominant_key_gives_its_value():
+    cfg, problem = _problem(head_dim=256, actual_history_len=512, seed=4)
+    qbits, pool, table, lens = _inputs(problem)
+    dec = pool.reshape(-1, 2, cfg.num_kv_heads, cfg.block_size, cfg.head_dim).copy()
+    # key 5 of page table[0, 0] aligned with row (0, 0, 0)'s query, scaled far above the rest
+    q = orc.decode_bfloat16(qbits[0, 0, 0])
+    code = torch.from_numpy((np.sign(q) * 448).astype(np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    dec[table[0, 0], 0, 0, 5] = code
+    out, _ = em.emulate_rows(qbits, dec.reshape(dec.shape[0], -1), table, lens, num_kv_heads=cfg.num_kv_heads,
+                             block_size=cfg.block_size, softmax_scale=cfg.softmax_scale, k_scale=problem.k_scale,
+                             v_scale=problem.v_scale, kernel="overlap", rows=np.array([[0, 0, 0]]))
+    v = orc.decode_e4m3fn(dec[table[0, 0], 1, 0, 5]) * problem.v_scale
+    np.testing.assert_allclose(out[0], v, rtol=0, atol=1e-9)
+
+
+def test_splits_merge_to_the_one_pass_result_without_rounding():
+    cfg, problem = _problem(head_dim=256, actual_history_len=1000)
+    one, lse1 = _model(cfg, problem, kernel="overlap", q_round=False, p_round=False)
+    three, lse3 = _model(cfg, problem, kernel="overlap", q_round=False, p_round=False, splits=3)
+    # (the fp32 exponent arguments round differently against other references)
+    np.testing.assert_allclose(three, one, rtol=0, atol=1e-6)
+    np.testing.assert_allclose(lse3, lse1, rtol=0, atol=1e-6)
+
+
+def test_mass_is_the_probability_sum_against_the_reference():
+    """mass = sum_k 2^(x_k - m) with m within 2.5 of the largest x_k; split
+    masses recombine against the largest range reference."""
+    cfg, problem = _problem(head_dim=256, actual_history_len=1000)
+    rows = np.array([[0, 1, 5], [1, 2, 60]])
+    _, lse, mass = _model(cfg, problem, kernel="overlap", exp2="exact", rows=rows, return_mass=True)
+    qbits, pool, table, lens = _inputs(problem)
+    shape = orc.OracleShape.from_config(cfg)
+    # natural-log sum of exp(score) over all keys vs log2 mass: mass * 2^m = sum 2^x
+    _, lse_plain = _model(cfg, problem, kernel="overlap", q_round=False, p_round=False, rows=rows)
+    for i in range(len(rows)):
+        # the largest probability (2^(x_max - m) in [1, 2^2.5]) bounds the mass from below
+        assert mass[i] >= 1.0
+    _, _, mass3 = _model(cfg, problem, kernel="overlap", exp2="exact", rows=rows, return_mass=True, splits=3)
+    np.testing.assert_allclose(mass3, mass, rtol=0.3)  # the same keys, rounded against other references
+    assert shape.head_dim == 256 and np.all(np.isfinite(lse_plain))

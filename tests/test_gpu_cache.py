@@ -97,6 +97,22 @@ def test_absmax_matches_torch(cuda_device):
         assert got == float(x.float().abs().max()), n
 
 
+def test_absmax_propagates_nan_like_torch(cuda_device):
+    """A NaN anywhere (either sign, any span of the reduction) gives NaN, as
+    torch's abs().max() does; infinities give inf."""
+    import math
+
+    gen = torch.Generator().manual_seed(6)
+    n = 4096 * 8 * 3 + 5
+    for where in (0, 1, 777, n // 2, n - 1):
+        for special in (float("nan"), -float("nan"), float("inf"), -float("inf")):
+            x = torch.randn(n, generator=gen).to(torch.bfloat16)
+            x[where] = special
+            want = float(x.float().abs().max())
+            got = float(absmax(x.to(cuda_device)))
+            assert math.isnan(want) == math.isnan(got) and (math.isnan(want) or got == want), (where, special, got)
+
+
 def test_e4m3_codes_match_torch_cast(cuda_device):
     """Round-to-nearest-even, the 448/464/480 boundary, subnormals, signed zeros,
     infinities and NaN: the producer's codes equal torch's float8_e4m3fn cast."""

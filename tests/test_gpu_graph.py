@@ -82,7 +82,7 @@ def test_graph_keeps_its_split_workspace(cuda_device):
     assert torch.equal(out, eager)
     assert (wider.float() - eager.float()).abs().max().item() < 2e-2  # same attention, another split
     # a caller-provided workspace gives the kept one's bits
-    ws = torch.empty(kernel.split_workspace_bytes(n_split), dtype=torch.uint8, device=cuda_device)
+    ws = torch.empty(kernel.workspace_bytes(n_split), dtype=torch.uint8, device=cuda_device)
     own = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, workspace=ws, **kw)
     torch.cuda.synchronize()
     assert torch.equal(own, eager)

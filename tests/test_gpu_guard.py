@@ -1,0 +1,289 @@
+"""The e4m3 MFMA path's error envelope and its precision guard, on the GPU.
+
+* ``precision="auto"`` (e4m3 MFMAs plus the guard) meets the bar (max-abs
+  2e-2, mean-abs 2e-3 against float64 attention on the dequantised cache)
+  where plain e4m3 MFMAs cannot: short runtime histories in a long bucket
+  (given as page lengths and as the reference's mask) and peaked score
+  distributions (Q scaled x2 and x3, K with a per-channel factor in [0.5, 2])
+  at 8K and 131K keys, aligned and not, with either exp2 mode.
+* ``precision="fp8"`` (no guard) matches the e4m3 numerical model
+  (oracle/e4m3_model.py) tightly: its larger errors on such data are the
+  method's rounding, not a kernel bug.  The same bound holds for the tile
+  kernel's e4m3 path at head_dim 64 and 128.
+* The guard recomputes exactly what the model says it should: rows of a
+  tile whose model mass is far above the threshold keep the e4m3 result bit
+  for bit, and a dense fixup equals the BF16-MFMA kernel.
+"""
+
+from __future__ import annotations
+
+import functools
+from dataclasses import replace
+
+import numpy as np
+import pytest
+import torch
+
+from aws_training_study_amd import _native
+from aws_training_study_amd.pcp_attention import make_history_attention_kernel
+from aws_training_study_amd.pcp_attention.config import PCPAttentionConfig
+from aws_training_study_amd.pcp_attention.inputs import make_block_valid_mask
+from aws_training_study_amd.pcp_attention.paging import page_valid_lengths
+from aws_training_study_amd.pcp_attention.workloads import build_paged_problem, get_workload
+from oracle import e4m3_model as em
+from oracle import pcp_oracle as orc
+
+from test_gpu_parity import MAX_ABS_TOL, MEAN_ABS_TOL
+
+pytestmark = pytest.mark.gpu
+
+FOUR = get_workload("four-chip-fp8").config   # 16 ranks, 8192-token history, D 256
+FULL = get_workload("full-fp8").config        # 64 ranks, 131072-token history, D 256
+
+
+@functools.lru_cache(maxsize=8)
+def _problem(cfg: PCPAttentionConfig, k_prescale: str, seed: int):
+    return build_paged_problem(cfg, seed, kv_scale="per_tensor", k_prescale=k_prescale)
+
+
+def _sample(cfg, count, seed):
+    rng = np.random.default_rng(seed)
+    rows = np.stack([rng.integers(0, cfg.pcp_size, count), rng.integers(0, cfg.num_q_heads, count),
+                     rng.integers(0, cfg.local_q_len, count)], axis=1)
+    corners = np.array([[0, 0, 0], [cfg.pcp_size - 1, cfg.num_q_heads - 1, cfg.local_q_len - 1]])
+    return np.concatenate([corners, rows])
+
+
+def _paged_reference(problem, q_stacked, rows, page_valid_len):
+    """float64 attention of the listed rows over exactly the pages' valid prefixes."""
+    cfg = problem.config
+    pool = orc.decode_e4m3fn(problem.kv_pages.view(torch.uint8).numpy()).reshape(
+        -1, 2, cfg.num_kv_heads, cfg.block_size, cfg.head_dim)
+    table = problem.block_table.numpy()
+    lens = page_valid_len.cpu().numpy()
+    keys, vals = [], []
+    for r in range(cfg.pcp_size):
+        for b in range(cfg.max_local_blocks):
+            n = min(int(lens[r, b]), cfg.block_size)
+            if n > 0:
+                keys.append(pool[table[r, b], 0, :, :n])
+                vals.append(pool[table[r, b], 1, :, :n])
+    k = np.concatenate(keys, axis=1) * problem.k_scale
+    v = np.concatenate(vals, axis=1) * problem.v_scale
+    q = orc.decode_bfloat16(q_stacked.view(torch.int16).numpy().view(np.uint16))
+    group = cfg.num_q_heads // cfg.num_kv_heads
+    out = np.empty((len(rows), cfg.head_dim))
+    for i, (rank, qh, tok) in enumerate(rows):
+        g = qh // group
+        out[i] = orc.dense_history_attention(q[rank, qh, tok][None, None, :], k[g:g + 1], v[g:g + 1],
+                                             cfg.softmax_scale)[0, 0]
+    return out
+
+
+def _model(problem, q_stacked, rows, page_valid_len, kernel="overlap", exp2="fast", **kw):
+    cfg = problem.config
+    return em.emulate_rows(q_stacked.view(torch.int16).numpy().view(np.uint16),
+                           problem.kv_pages.view(torch.uint8).numpy(), problem.block_table.numpy(),
+                           page_valid_len.cpu().numpy(), num_kv_heads=cfg.num_kv_heads, block_size=cfg.block_size,
+                           softmax_scale=cfg.softmax_scale, k_scale=problem.k_scale, v_scale=problem.v_scale,
+                           kernel=kernel, exp2=exp2, rows=rows, **kw)
+
+
+def _scaled_q(problem, factor):
+    return problem.q_stacked if factor == 1 else (problem.q_stacked.float() * factor).to(torch.bfloat16)
+
+
+def _pick(out, rows):
+    got = out.float().cpu().numpy()
+    return np.stack([got[r, h, t] for r, h, t in rows])
+
+
+def _check_bar(got, want, label):
+    max_abs, mean_abs = orc.max_abs_and_mean_abs(got, want)
+    print(f"{label}: max_abs={max_abs:.3e} mean_abs={mean_abs:.3e}", flush=True)
+    assert np.isfinite(got).all(), label
+    assert max_abs <= MAX_ABS_TOL and mean_abs <= MEAN_ABS_TOL, label
+
+
+def _check_model(got, model, mass, label):
+    """The kernel against the model of its own arithmetic: a bf16 rounding of
+    the output plus fp32 accumulation-order noise, on rows with a
+    probability mass of at least 64.  (With fewer effective keys one e4m3
+    code that the MFMA's fp32 accumulation rounds the other way moves the
+    output by a large fraction of the key's weight; those rows are reported.)"""
+    diff = np.abs(got - model)
+    excess = diff - np.abs(model) * 2.0 ** -8
+    ok = mass >= 64
+    print(f"{label}: vs e4m3 model on {ok.sum()} of {len(ok)} rows max={diff[ok].max(initial=0):.3e} "
+          f"excess over bf16 rounding={excess[ok].max(initial=0):.3e} mean={diff[ok].mean() if ok.any() else 0:.3e}; "
+          f"low-mass rows max={diff[~ok].max(initial=0):.3e}", flush=True)
+    if ok.any():
+        assert excess[ok].max() <= 5e-3, label
+        assert diff[ok].mean() <= 2e-4 + np.abs(model[ok]).mean() * 2.0 ** -9, label
+
+
+# ---- short runtime histories in a long bucket (VERDICT: auto from runtime lengths)
+
+
+@pytest.mark.parametrize("bucket", ["four-chip", "full"])
+@pytest.mark.parametrize("tokens", [785, 1500, 4096])
+def test_auto_on_short_runtime_history_page_lengths(bucket, tokens, cuda_device):
+    cfg = FOUR if bucket == "four-chip" else FULL
+    problem = _problem(cfg, "none", 41)
+    lens = page_valid_lengths(replace(cfg, actual_history_len=tokens))
+    print(f"case {bucket} bucket {cfg.max_history_len}, runtime {tokens} tokens (page_valid_len)", flush=True)
+    gpu = problem.to(cuda_device)
+    kernel = make_history_attention_kernel(cfg)
+    out = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=lens.to(cuda_device),
+                 k_scale=problem.k_scale, v_scale=problem.v_scale)
+    torch.cuda.synchronize()
+    rows = _sample(cfg, 160, tokens)
+    _check_bar(_pick(out, rows), _paged_reference(problem, problem.q_stacked, rows, lens),
+               f"{bucket} runtime {tokens} auto")
+
+
+@pytest.mark.parametrize("bucket,tokens", [("four-chip", 1024), ("four-chip", 4096), ("full", 4096), ("full", 8192)])
+def test_auto_on_short_runtime_history_reference_mask(bucket, tokens, cuda_device):
+    """The reference's mask form (run_poc.py:137-153) on the GPU: converted on
+    the device, same result as the page-length form."""
+    cfg = FOUR if bucket == "four-chip" else FULL
+    problem = _problem(cfg, "none", 41)
+    runtime = replace(cfg, actual_history_len=tokens)
+    mask = make_block_valid_mask(runtime).to(cuda_device)
+    print(f"case {bucket} bucket {cfg.max_history_len}, runtime {tokens} tokens (mask)", flush=True)
+    gpu = problem.to(cuda_device)
+    kernel = make_history_attention_kernel(cfg)
+    out = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, mask, k_scale=problem.k_scale,
+                 v_scale=problem.v_scale)
+    lens = page_valid_lengths(runtime)
+    ref_out = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=lens.to(cuda_device),
+                     k_scale=problem.k_scale, v_scale=problem.v_scale)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_out)
+    rows = _sample(cfg, 160, tokens + 1)
+    _check_bar(_pick(out, rows), _paged_reference(problem, problem.q_stacked, rows, lens),
+               f"{bucket} runtime {tokens} mask auto")
+
+
+# ---- peaked scores (VERDICT: e4m3 away from unit-normal data)
+
+PEAKED = [("none", 2), ("none", 3), ("per_channel", 1), ("per_channel", 2), ("per_channel", 3)]
+
+
+@pytest.mark.parametrize("k_prescale,q_factor", PEAKED)
+@pytest.mark.parametrize("tokens,exp2", [(8192, "fast"), (8000, "exact"), (8000, "fast"), (8192, "exact")])
+def test_peaked_scores_8k(k_prescale, q_factor, tokens, exp2, cuda_device):
+    cfg = replace(FOUR, actual_history_len=tokens).validate()
+    _peaked_case(cfg, k_prescale, q_factor, exp2, cuda_device, rows=192)
+
+
+@pytest.mark.parametrize("k_prescale,q_factor", [("none", 2), ("none", 3), ("per_channel", 1), ("per_channel", 3)])
+@pytest.mark.parametrize("tokens,exp2", [(131072, "fast"), (131000, "exact")])
+def test_peaked_scores_131k(k_prescale, q_factor, tokens, exp2, cuda_device):
+    cfg = replace(FULL, actual_history_len=tokens).validate()
+    _peaked_case(cfg, k_prescale, q_factor, exp2, cuda_device, rows=48)
+
+
+def _peaked_case(cfg, k_prescale, q_factor, exp2, device, rows):
+    problem = _problem(cfg, k_prescale, 43)
+    q = _scaled_q(problem, q_factor)
+    label = f"L={cfg.actual_history_len} K {k_prescale} Q x{q_factor} exp2 {exp2}"
+    print(f"case {label}", flush=True)
+    gpu = problem.to(device)
+    qd = q.to(device)
+    kernel = make_history_attention_kernel(cfg)
+    kw = dict(page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale, v_scale=problem.v_scale, exp2=exp2)
+    auto = kernel(qd, gpu.kv_pages, gpu.block_table, **kw)
+    fp8 = kernel(qd, gpu.kv_pages, gpu.block_table, precision="fp8", splits=1, **kw)
+    torch.cuda.synchronize()
+    sample = _sample(cfg, rows, cfg.actual_history_len + q_factor)
+    ref = _paged_reference(problem, q, sample, problem.page_valid_len)
+    model, _, mass = _model(problem, q, sample, problem.page_valid_len, exp2=exp2, return_mass=True)
+    e4m3_max, e4m3_mean = orc.max_abs_and_mean_abs(_pick(fp8, sample), ref)
+    print(f"{label}: e4m3 alone max_abs={e4m3_max:.3e} mean_abs={e4m3_mean:.3e}; rows below the guard mass "
+          f"{(mass < _native.GUARD_MIN_MASS).mean():.2f}", flush=True)
+    _check_model(_pick(fp8, sample), model, mass, f"{label} fp8")
+    _check_bar(_pick(auto, sample), ref, f"{label} auto")
+
+
+# ---- the tile kernel's e4m3 path (head_dim 64 / 128) against the model
+
+
+@pytest.mark.parametrize("head_dim,tokens", [(64, 700), (128, 3000), (128, 8192)])
+def test_tile_kernel_e4m3_matches_model(head_dim, tokens, cuda_device):
+    cfg = PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=8192, actual_history_len=tokens,
+                             block_size=256, interleave_size=64, num_q_heads=16, num_kv_heads=2, head_dim=head_dim,
+                             backend="hip").validate()
+    problem = _problem(cfg, "none", 44)
+    print(f"case tile e4m3 D={head_dim} L={tokens}", flush=True)
+    gpu = problem.to(cuda_device)
+    kernel = make_history_attention_kernel(cfg)
+    kw = dict(page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale, v_scale=problem.v_scale)
+    fp8 = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, precision="fp8", splits=1, **kw)
+    auto = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, **kw)
+    torch.cuda.synchronize()
+    rows = _sample(cfg, 256, tokens)
+    model, _, mass = _model(problem, problem.q_stacked, rows, problem.page_valid_len, kernel="tile", exp2="exact",
+                            return_mass=True)
+    _check_model(_pick(fp8, rows), model, mass, f"tile D={head_dim} L={tokens} fp8")
+    _check_bar(_pick(auto, rows), _paged_reference(problem, problem.q_stacked, rows, problem.page_valid_len),
+               f"tile D={head_dim} L={tokens} auto")
+
+
+# ---- what the guard recomputes
+
+
+def test_guard_keeps_e4m3_rows_of_unflagged_tiles_bit_for_bit(cuda_device):
+    """Q x1.2 on the 8K workload: some rows fall below the guard mass.  Tiles
+    (128 rows of one KV head) whose every row's model mass is above 1.25x the
+    threshold are not recomputed: their output is the e4m3 pass's, bit for
+    bit; the tiles holding a row below 0.8x are recomputed with BF16 MFMAs."""
+    cfg = FOUR
+    problem = _problem(cfg, "none", 45)
+    q = _scaled_q(problem, 1.2)
+    gpu = problem.to(cuda_device)
+    qd = q.to(cuda_device)
+    kernel = make_history_attention_kernel(cfg)
+    kw = dict(page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale, v_scale=problem.v_scale, splits=1)
+    auto = kernel(qd, gpu.kv_pages, gpu.block_table, **kw).float().cpu().numpy()
+    fp8 = kernel(qd, gpu.kv_pages, gpu.block_table, precision="fp8", **kw).float().cpu().numpy()
+    bf16 = kernel(qd, gpu.kv_pages, gpu.block_table, precision="bf16", **kw).float().cpu().numpy()
+    torch.cuda.synchronize()
+    group = cfg.num_q_heads // cfg.num_kv_heads
+    per_head = cfg.pcp_size * group * cfg.local_q_len // 128
+    # the model's mass of every row, in the kernels' tile order
+    _, _, mass = _model(problem, q, None, problem.page_valid_len, return_mass=True)
+    T = _native.GUARD_MIN_MASS
+    by_tile = mass.reshape(cfg.pcp_size, cfg.num_kv_heads, group, cfg.local_q_len).transpose(1, 0, 2, 3)
+    by_tile = by_tile.reshape(cfg.num_kv_heads, per_head, 128).min(axis=2)
+    kept = recomputed = 0
+    for g in range(cfg.num_kv_heads):
+        for tile in range(per_head):
+            head_rows = tile * 128 + np.arange(128)
+            rank, rem = np.divmod(head_rows, group * cfg.local_q_len)
+            hig, tok = np.divmod(rem, cfg.local_q_len)
+            sel = (rank, g * group + hig, tok)
+            if by_tile[g, tile] > 1.25 * T:
+                kept += 1
+                assert np.array_equal(auto[sel], fp8[sel]), f"tile {g}/{tile} recomputed"
+            elif by_tile[g, tile] < 0.8 * T:
+                recomputed += 1
+                assert np.abs(auto[sel] - bf16[sel]).max() <= 2e-3, f"tile {g}/{tile} not recomputed"
+    print(f"tiles kept {kept}, recomputed {recomputed} of {cfg.num_kv_heads * per_head}", flush=True)
+    assert kept > 0 and recomputed > 0
+
+
+def test_dense_fixup_equals_the_bf16_kernel(cuda_device):
+    """Q x4: every row is flagged, the plan goes dense (one pass per tile),
+    and the result is the BF16-MFMA kernel's, bit for bit."""
+    cfg = FOUR
+    problem = _problem(cfg, "none", 46)
+    q = _scaled_q(problem, 4).to(cuda_device)
+    gpu = problem.to(cuda_device)
+    kernel = make_history_attention_kernel(cfg)
+    kw = dict(page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale, v_scale=problem.v_scale, splits=1)
+    auto, lse = kernel(q, gpu.kv_pages, gpu.block_table, return_lse=True, **kw)
+    bf16, lse16 = kernel(q, gpu.kv_pages, gpu.block_table, precision="bf16", return_lse=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(auto, bf16)
+    assert torch.equal(lse, lse16)

@@ -4,10 +4,14 @@ float64 oracle on every output row.
 Each case draws pcp size, interleave, block size, heads, head dim, cache
 dtype, MFMA precision and a runtime history length (generally not aligned to
 anything) from a fixed seed, so the set is the same on every run.  Bar:
-max-abs <= 2e-2 and mean-abs <= 2e-3, except that e4m3 MFMAs over short
-histories (where the e4m3 rounding of Q and P is not averaged away) are
-held to the one-pass kernel's own error (same exp2 mode) plus 4e-3 when the
-bar is missed.
+max-abs <= 2e-2 and mean-abs <= 2e-3 for every case on BF16 MFMAs and under
+``precision="auto"`` (e4m3 MFMAs with the precision guard).  Explicit
+``precision="fp8"`` (no guard) over short histories can miss it: the e4m3
+rounding of Q and P is not averaged away over few keys.  Such a case must
+then match the e4m3 numerical model of its kernel (oracle/e4m3_model.py) to
+within the output's bf16 rounding plus 5e-3 on every row with a probability
+mass of 64 or more, which shows the miss is the method's rounding and
+nothing else.
 """
 
 from __future__ import annotations
@@ -21,6 +25,7 @@ import torch
 from aws_training_study_amd.pcp_attention import make_history_attention_kernel
 from aws_training_study_amd.pcp_attention.config import PCPAttentionConfig
 from aws_training_study_amd.pcp_attention.workloads import build_paged_problem
+from oracle import e4m3_model as em
 from oracle import pcp_oracle as orc
 
 from test_gpu_parity import MAX_ABS_TOL, MEAN_ABS_TOL, _real_history
@@ -54,9 +59,9 @@ def _draw(i: int) -> tuple[PCPAttentionConfig, str, dict]:
                                      backend="hip").validate()
         except ValueError:
             continue
-        precision = str(rng.choice(["fp8", "fp8", "bf16"])) if kv_dtype == "fp8_e4m3fn" else "auto"
+        precision = str(rng.choice(["auto", "fp8", "bf16"])) if kv_dtype == "fp8_e4m3fn" else "auto"
         kw = {"precision": precision}
-        if precision == "fp8" and d == 256:
+        if precision != "bf16" and kv_dtype == "fp8_e4m3fn" and d == 256:
             kw["exp2"] = str(rng.choice(["fast", "exact"]))
             kw["splits"] = int(rng.choice([1, 1, 2, 3]))
         return cfg, kv_dtype, kw
@@ -83,11 +88,23 @@ def test_random_configuration(i, cuda_device):
     print(f"  max_abs={max_abs:.3e} mean_abs={mean_abs:.3e}", flush=True)
     if max_abs <= MAX_ABS_TOL and mean_abs <= MEAN_ABS_TOL:
         return
-    assert kw.get("precision") == "fp8", "BF16 MFMA path outside the bar"
-    one = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len,
-                 k_scale=problem.k_scale, v_scale=problem.v_scale, **{**kw, "splits": 1})
-    torch.cuda.synchronize()
-    one_max, one_mean = orc.max_abs_and_mean_abs(one.float().cpu().numpy(), exp)
-    print(f"  short-history e4m3 case: one-pass max_abs={one_max:.3e} mean_abs={one_mean:.3e}", flush=True)
-    assert cfg.actual_history_len < 2048, "e4m3 path outside the bar on a long history"
-    assert max_abs <= one_max + 4e-3 and mean_abs <= max(MEAN_ABS_TOL, one_mean + 1e-3)
+    assert kw.get("precision") == "fp8", "BF16 or guarded path outside the bar"
+    # the split count the call ran with (given, or the kernel's own choice)
+    splits = kw["splits"] if "splits" in kw else kernel.split_count(cuda_device, False)
+    model, _, mass = em.emulate_rows(problem.q_stacked.view(torch.int16).numpy().view(np.uint16),
+                                     problem.kv_pages.view(torch.uint8).numpy(), problem.block_table.numpy(),
+                                     problem.page_valid_len.numpy(), num_kv_heads=cfg.num_kv_heads,
+                                     block_size=cfg.block_size, softmax_scale=cfg.softmax_scale,
+                                     k_scale=problem.k_scale, v_scale=problem.v_scale,
+                                     kernel="overlap" if cfg.head_dim == 256 else "tile",
+                                     exp2=kw.get("exp2", "fast") if cfg.head_dim == 256 else "exact",
+                                     splits=int(splits), return_mass=True)
+    # rows with fewer effective keys: one e4m3 code rounded the other way by
+    # the MFMA's fp32 accumulation moves the output a lot; checked from 64 on
+    ok = np.broadcast_to(mass[..., None] >= 64, got.shape)
+    diff = np.abs(got - model)[ok]
+    excess = diff - np.abs(model[ok]) * 2.0 ** -8
+    print(f"  e4m3 case outside the bar: vs e4m3 model on {ok.mean():.2f} of the rows max={diff.max(initial=0):.3e} "
+          f"excess={excess.max(initial=0):.3e}", flush=True)
+    if diff.size:
+        assert excess.max() <= 5e-3 and diff.mean() <= 2e-4 + np.abs(model[ok]).mean() * 2.0 ** -9
