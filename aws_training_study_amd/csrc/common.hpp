@@ -76,20 +76,24 @@ struct FwdArgs {
     uint8_t* guard_out;
     float guard_min_mass;
     // The BF16 fixup of a guarded launch (history_fwd_kernel<..., FIXUP>):
-    // the plan of guard_plan_kernel ([0] listed tiles, [1] mode, then the
-    // list of KV head * row_tiles + row tile ids) and, in sparse mode, the
-    // partials' capacity in tiles (part_o / part_lse hold [splits,
+    // the plan of guard_plan_kernel (below) and, in sparse mode, the
+    // partials' capacity in 128-row groups (part_o / part_lse hold [splits,
     // guard_slots * 128] rows).
     const int32_t* guard_plan;
     int32_t guard_slots;
 };
 
-// Modes of a guard plan: no flagged row, few flagged tiles (history split
-// across workgroups, partials merged), or many (one pass per tile).
+// Modes of a guard plan: no flagged row, few flagged rows (history split
+// across workgroups, partials merged), or many (one pass per group).
 constexpr int kGuardNone = 0;
 constexpr int kGuardSparse = 1;
 constexpr int kGuardDense = 2;
-constexpr int kGuardPlanHeader = 4;
+// A plan: [0] 128-row groups, [1] mode, [2 + h] first group of KV head h
+// ([2 + num_kv_heads] = [0]), then, from guard_list_offset, the gathered
+// rows (head row indices, -1 padding), 128 per group.
+__host__ __device__ __forceinline__ int guard_list_offset(int num_kv_heads) {
+    return (2 + num_kv_heads + 1 + 3) / 4 * 4;
+}
 
 // ln(E[(1 + f) / 2^f]) for f uniform in [0, 1): how much the linear-mantissa
 // exp2 of the FP8 overlap kernel overestimates a sum of exponentials on

@@ -2,13 +2,13 @@
 // fixup and the merge of its split partials.
 //
 // The e4m3 pass writes one flag byte per query row (probability mass below
-// PCPA_GUARD_MIN_MASS).  guard_plan_kernel lists the 128-row tiles (of the
-// BF16 tile kernel: 4 waves x 32 rows of one KV head) that hold a flagged
-// row.  Few tiles: sparse mode, where the fixup splits each tile's history
-// walk over several workgroups (bounded latency) and guard_merge_kernel
-// combines the ranges; many tiles: dense mode, one workgroup per tile,
-// writing the output directly.  With no flagged row every fixup and merge
-// workgroup exits at once.
+// PCPA_GUARD_MIN_MASS).  guard_plan_kernel gathers the flagged rows of each
+// KV head into groups of 128 (the BF16 tile kernel's 4 waves x 32 rows).
+// Few groups: sparse mode, where the fixup splits each group's history walk
+// over several workgroups (bounded latency) and guard_merge_kernel combines
+// the ranges; many: dense mode, one workgroup per group, writing the output
+// directly.  With no flagged row every fixup and merge workgroup exits at
+// once.
 #pragma once
 
 #include "common.hpp"
@@ -16,7 +16,8 @@
 namespace pcpa {
 
 constexpr int kGuardPlanThreads = 1024;
-constexpr int kTileWindow = 16384;
+// KV heads a guard plan handles (the guarded launch is refused beyond).
+constexpr int kGuardMaxHeads = 64;
 // Capacity of the sparse partials, in query rows over all history ranges:
 // [splits, slots * 128] FP32 rows of D + 1 values (67 MB at head_dim 256).
 constexpr int64_t kGuardPartialRows = 65536;
@@ -27,11 +28,11 @@ struct GuardShape {
     int32_t group_rows;   // group * local_q
     int32_t local_q;
     int32_t num_q_heads;
+    int32_t num_kv_heads;
     int32_t group;
-    int32_t row_tiles;    // 128-row tiles per KV head
-    int32_t tiles_total;  // row_tiles * num_kv_heads
-    int32_t max_sparse;   // tiles the sparse partials hold
+    int32_t max_sparse;   // 128-row groups the sparse partials hold
 };
+
 
 // Flag-array index ([pcp, Hq, local_q] order) of row r of KV head `head`
 // (rows of a head in the kernels' order: rank, Q head of the group, token).
@@ -43,20 +44,81 @@ __device__ __forceinline__ int64_t guard_row_index(const GuardShape& g, int head
     return ((int64_t)(rank * g.num_q_heads + head * g.group + hig)) * g.local_q + tok;
 }
 
-// One workgroup.  plan[0] = listed tiles, plan[1] = mode, plan[4 + i] = tile
-// id (KV head * row_tiles + row tile) of the i-th flagged tile, ascending.
+// Block-wide exclusive prefix of x over the workgroup's threads (thread
+// order), and the total.  Uses `wave_sum` (kGuardPlanThreads / 64 ints).
+__device__ __forceinline__ int block_exclusive_scan(int x, int* wave_sum, int& total) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int incl = x;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off);
+        if (lane >= off) incl += y;
+    }
+    if (lane == 63) wave_sum[wave] = incl;
+    __syncthreads();
+    int before = 0;
+    total = 0;
+    for (int w = 0; w < kGuardPlanThreads / 64; ++w) {
+        before += w < wave ? wave_sum[w] : 0;
+        total += wave_sum[w];
+    }
+    __syncthreads();  // wave_sum is rewritten by the next scan
+    return before + incl - x;
+}
+
+// One workgroup.  Lists every flagged row, grouped by KV head: head h's rows
+// (in the kernels' order: rank, Q head of the group, token) fill its segment
+// of the list in ascending order, padded with -1 to a multiple of 128 rows.
+// plan[0] = 128-row groups, plan[1] = mode, plan[2 + h] = first group of
+// head h (h < num_kv_heads, plan[2 + num_kv_heads] = plan[0]), then the
+// list (plan + guard_list_offset) of head rows.  Deterministic.
 __global__ void __launch_bounds__(kGuardPlanThreads) guard_plan_kernel(const uint8_t* flags, GuardShape g,
                                                                       int32_t* plan) {
-    __shared__ int wave_count[kGuardPlanThreads / 64];
+    __shared__ int wave_sum[kGuardPlanThreads / 64];
+    __shared__ int head_count[kGuardMaxHeads];
+    __shared__ int next[kGuardMaxHeads];  // head h's next free list position
     const int tid = threadIdx.x;
-    // ---- any flag at all (16-byte loads; the common case ends here) ------
+    const int heads = g.num_kv_heads;
+    for (int i = tid; i < kGuardMaxHeads; i += kGuardPlanThreads) head_count[i] = 0;
+    __syncthreads();
+    // Rows are visited in [pcp, Hq, local_q] order, `unit` consecutive rows
+    // at a time (16 when local_q is a multiple of 16: one 16-byte load, one
+    // Q head; else 1); restricted to KV head h that is head h's row order.
+    const bool chunked = (g.local_q & 15) == 0;
+    const int unit = chunked ? 16 : 1;
+    const int64_t units = g.rows_total / unit;
+    // flagged rows of unit u, one bit each, and the unit's KV head and head row
+    auto load_unit = [&](int64_t u, int& head, int& head_row) -> uint32_t {
+        const int64_t row = u * unit;
+        uint32_t bits = 0;
+        if (chunked) {
+            const v4i x = *(const v4i*)(flags + row);
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    if (((uint32_t)x[w] >> (8 * b)) & 0xffu) bits |= 1u << (4 * w + b);
+        } else {
+            bits = flags[row] ? 1u : 0u;
+        }
+        const int64_t rh = row / g.local_q;
+        const int tok = (int)(row - rh * g.local_q);
+        const int rank = (int)(rh / g.num_q_heads);
+        const int qh = (int)(rh - (int64_t)rank * g.num_q_heads);
+        head = qh / g.group;
+        head_row = (rank * g.group + (qh - head * g.group)) * g.local_q + tok;
+        return bits;
+    };
+    // ---- count each head's flagged rows (the common case: none, done) -----
     int any = 0;
-    const int64_t vecs = g.rows_total / 16;
-    for (int64_t i = tid; i < vecs; i += kGuardPlanThreads) {
-        const v4i x = *(const v4i*)(flags + 16 * i);
-        any |= x[0] | x[1] | x[2] | x[3];
+    for (int64_t u = tid; u < units; u += kGuardPlanThreads) {
+        int head, head_row;
+        const uint32_t bits = load_unit(u, head, head_row);
+        if (bits) {
+            any = 1;
+            atomicAdd(&head_count[head], __builtin_popcount(bits));
+        }
     }
-    for (int64_t i = vecs * 16 + tid; i < g.rows_total; i += kGuardPlanThreads) any |= flags[i];
     if (!__syncthreads_or(any)) {
         if (tid == 0) {
             plan[0] = 0;
@@ -64,72 +126,62 @@ __global__ void __launch_bounds__(kGuardPlanThreads) guard_plan_kernel(const uin
         }
         return;
     }
-    // ---- list the tiles holding a flagged row, in tile order --------------
-    // Tile flags are gathered in LDS a window of kTileWindow tiles at a time.
-    // When local_q is a multiple of 16, 16 consecutive flag bytes (one Q
-    // head's tokens t..t+15 of one rank) belong to one tile and are read as
-    // one 16-byte load; otherwise the window's rows are read byte by byte.
-    __shared__ uint8_t tile_hit[kTileWindow];
-    const int lane = tid & 63, wave = tid >> 6;
-    const bool chunked = (g.local_q & 15) == 0;
-    int listed = 0;
-    for (int w0 = 0; w0 < g.tiles_total; w0 += kTileWindow) {
-        const int w1 = min(w0 + kTileWindow, g.tiles_total);
-        for (int i = tid; i < kTileWindow; i += kGuardPlanThreads) tile_hit[i] = 0;
-        __syncthreads();
-        if (chunked) {
-            for (int64_t c = tid; c < vecs; c += kGuardPlanThreads) {
-                const v4i x = *(const v4i*)(flags + 16 * c);
-                if (!(x[0] | x[1] | x[2] | x[3])) continue;
-                const int64_t row = 16 * c;  // [pcp, Hq, local_q] index
-                const int64_t rh = row / g.local_q;
-                const int tok = (int)(row - rh * g.local_q);
-                const int rank = (int)(rh / g.num_q_heads);
-                const int qh = (int)(rh - (int64_t)rank * g.num_q_heads);
-                const int head = qh / g.group;
-                const int head_row = (rank * g.group + (qh - head * g.group)) * g.local_q + tok;
-                const int id = head * g.row_tiles + head_row / kRowsPerGroup;
-                if (id >= w0 && id < w1) tile_hit[id - w0] = 1;
-            }
-        } else {
-            for (int id = w0 + tid; id < w1; id += kGuardPlanThreads) {
-                const int head = id / g.row_tiles;
-                const int r0 = (id - head * g.row_tiles) * kRowsPerGroup;
-                const int r1 = min(r0 + kRowsPerGroup, g.rows_per_head);
-                int hit = 0;
-                for (int r = r0; r < r1; ++r) hit |= flags[guard_row_index(g, head, r)];
-                tile_hit[id - w0] = hit ? 1 : 0;
-            }
-        }
-        __syncthreads();
-        for (int base = w0; base < w1; base += kGuardPlanThreads) {
-            const int id = base + tid;
-            const bool hit = id < w1 && tile_hit[id - w0];
-            const uint64_t ballot = __builtin_amdgcn_ballot_w64(hit);
-            if (lane == 0) wave_count[wave] = __builtin_popcountll(ballot);
-            __syncthreads();
-            int before = listed, total = 0;
-            for (int w = 0; w < kGuardPlanThreads / 64; ++w) {
-                before += w < wave ? wave_count[w] : 0;
-                total += wave_count[w];
-            }
-            if (hit) {
-                const uint64_t below = lane ? ballot & (~0ull >> (64 - lane)) : 0ull;
-                plan[kGuardPlanHeader + before + __builtin_popcountll(below)] = id;
-            }
-            listed += total;
-            __syncthreads();  // wave_count (and, after the window, tile_hit) is rewritten next
-        }
-    }
+    int32_t* const list = plan + guard_list_offset(heads);
     if (tid == 0) {
-        plan[0] = listed;
-        plan[1] = listed <= g.max_sparse ? kGuardSparse : kGuardDense;
+        int first = 0;
+        for (int h = 0; h < heads; ++h) {
+            plan[2 + h] = first;
+            next[h] = first * kRowsPerGroup;
+            first += (head_count[h] + kRowsPerGroup - 1) / kRowsPerGroup;
+        }
+        plan[2 + heads] = first;
+        plan[0] = first;
+        plan[1] = first <= g.max_sparse ? kGuardSparse : kGuardDense;
+    }
+    __syncthreads();
+    // -1 padding of every segment's last group
+    for (int h = 0; h < heads; ++h) {
+        const int padded = (head_count[h] + kRowsPerGroup - 1) / kRowsPerGroup * kRowsPerGroup;
+        for (int i = head_count[h] + tid; i < padded; i += kGuardPlanThreads) list[next[h] + i] = -1;
+    }
+    // ---- write the rows in order: kUnits consecutive units per thread -----
+    constexpr int kUnits = 4;
+    for (int64_t c0 = 0; c0 < units; c0 += (int64_t)kGuardPlanThreads * kUnits) {
+        uint32_t bits[kUnits];
+        int head[kUnits], head_row[kUnits];
+        bool mine = false;
+#pragma unroll
+        for (int i = 0; i < kUnits; ++i) {
+            const int64_t u = c0 + (int64_t)tid * kUnits + i;
+            bits[i] = 0;
+            head[i] = -1;
+            head_row[i] = 0;
+            if (u < units) bits[i] = load_unit(u, head[i], head_row[i]);
+            mine |= bits[i] != 0;
+        }
+        if (!__syncthreads_or(mine)) continue;
+        for (int h = 0; h < heads; ++h) {
+            int count = 0;
+#pragma unroll
+            for (int i = 0; i < kUnits; ++i) count += head[i] == h ? __builtin_popcount(bits[i]) : 0;
+            int total;
+            const int pos = block_exclusive_scan(count, wave_sum, total);
+            if (count) {
+                int k = next[h] + pos;
+#pragma unroll
+                for (int i = 0; i < kUnits; ++i)
+                    if (head[i] == h)
+                        for (uint32_t b = bits[i]; b; b &= b - 1) list[k++] = head_row[i] + __builtin_ctz(b);
+            }
+            __syncthreads();  // every read of next[h] is done
+            if (tid == 0) next[h] += total;
+        }
     }
 }
 
 // Sparse mode: one thread per (slot row, 8 consecutive d) merges the splits'
-// partials of the listed tiles' rows by log-sum-exp (as merge_splits_kernel)
-// into out (bf16) and lse.  Other modes, or slots past the list: nothing.
+// partials of a listed row by log-sum-exp (as merge_splits_kernel) into out
+// (bf16) and lse.  Other modes, padding and slots past the list: nothing.
 __global__ void __launch_bounds__(256) guard_merge_kernel(const float* part_o, const float* part_lse, int splits,
                                                           const int32_t* plan, GuardShape g, int d_vec8, uint8_t* out,
                                                           float* lse_out) {
@@ -138,18 +190,21 @@ __global__ void __launch_bounds__(256) guard_merge_kernel(const float* part_o, c
     const int64_t slot_row = idx / d_vec8;
     const int slot = (int)(slot_row / kRowsPerGroup);
     if (slot >= plan[0]) return;
-    const int id = plan[kGuardPlanHeader + slot];
-    const int head = id / g.row_tiles;
-    const int r = (id - head * g.row_tiles) * kRowsPerGroup + (int)(slot_row - (int64_t)slot * kRowsPerGroup);
-    if (r >= g.rows_per_head) return;
+    const int r = plan[guard_list_offset(g.num_kv_heads) + slot_row];
+    if (r < 0) return;
+    int head = 0;
+    while (plan[2 + head + 1] <= slot) ++head;
     const int64_t row = guard_row_index(g, head, r);
     const int D = d_vec8 * 8;
     const int d0 = (int)(idx - slot_row * d_vec8) * 8;
     const int64_t stride = (int64_t)g.max_sparse * kRowsPerGroup;  // rows of one split's partials
+    // (unrolled so that several ranges' loads are in flight together)
     float mx = -INFINITY;
+#pragma unroll 8
     for (int sp = 0; sp < splits; ++sp) mx = fmaxf(mx, part_lse[sp * stride + slot_row]);
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float wsum = 0.f;
+#pragma unroll 4
     for (int sp = 0; sp < splits; ++sp) {
         const float l = part_lse[sp * stride + slot_row];
         const float w = l == -INFINITY ? 0.f : __expf(l - mx);

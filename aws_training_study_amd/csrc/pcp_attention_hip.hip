@@ -72,7 +72,7 @@ inline FwdArgs common_args(const pcpa_params* p, const void* q, void* out) {
 // row flags, the fixup plan and the fixup's split partials.
 struct WorkspaceLayout {
     int64_t part_o, part_lse, part_m, flags, plan, gpart_o, gpart_lse, bytes;
-    int32_t guard_splits, guard_slots, tiles_total;
+    int32_t guard_splits, guard_slots, groups_total;
 };
 
 inline bool guarded(const pcpa_params* p) { return (p->flags & PCPA_FLAG_PRECISION_GUARD) != 0; }
@@ -89,21 +89,23 @@ inline WorkspaceLayout workspace_layout(const pcpa_params* p, int splits) {
         w.bytes = w.part_m + (int64_t)splits * rows * 4;
     }
     if (guarded(p)) {
-        // fixup: 128-row tiles of the BF16 tile kernel; the history's key
-        // tiles cut into ranges of at least 4 (256 keys), at most 32, so that
-        // a few flagged tiles cost a short walk rather than a whole history's
+        // fixup: the flagged rows gathered into groups of 128 (at most as
+        // many groups as 128-row tiles); the history's key tiles cut into
+        // ranges of at least 4 (256 keys), at most 64, so that a few flagged
+        // rows cost a short walk rather than a whole history's
         const int64_t entries = (int64_t)p->pcp_size * p->max_local_blocks;
         const int64_t key_tiles = entries * (p->block_size / kKeyTile);
         const int64_t rows_per_head = rows / p->num_q_heads * (p->num_q_heads / p->num_kv_heads);
-        w.tiles_total = (int32_t)((rows_per_head + kRowsPerGroup - 1) / kRowsPerGroup * p->num_kv_heads);
+        w.groups_total = (int32_t)((rows_per_head + kRowsPerGroup - 1) / kRowsPerGroup * p->num_kv_heads);
         int64_t gs = key_tiles / 4;
-        gs = gs < 1 ? 1 : gs > 32 ? 32 : gs;
+        gs = gs < 1 ? 1 : gs > 64 ? 64 : gs;
         w.guard_splits = (int32_t)gs;
         const int64_t slots = kGuardPartialRows / kRowsPerGroup / gs;
-        w.guard_slots = (int32_t)(slots < w.tiles_total ? slots : w.tiles_total);
+        w.guard_slots = (int32_t)(slots < w.groups_total ? slots : w.groups_total);
         w.flags = align16(w.bytes);
         w.plan = align16(w.flags + rows);
-        w.gpart_o = align16(w.plan + (int64_t)(kGuardPlanHeader + w.tiles_total) * 4);
+        w.gpart_o = align16(w.plan + ((int64_t)guard_list_offset(p->num_kv_heads) +
+                                      (int64_t)w.groups_total * kRowsPerGroup) * 4);
         const int64_t prow = (int64_t)w.guard_splits * w.guard_slots * kRowsPerGroup;
         w.gpart_lse = w.gpart_o + prow * p->head_dim * 4;
         w.bytes = w.gpart_lse + prow * 4;
@@ -167,6 +169,7 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
     const bool fp8 = store8 && !(p->flags & PCPA_FLAG_BF16_MFMA);
     const bool overlap = fp8 && p->head_dim == 256;
     const bool guard = fp8 && guarded(p);
+    if (guard && p->num_kv_heads > kGuardMaxHeads) return PCPA_ERR_UNSUPPORTED;
     const WorkspaceLayout w = workspace_layout(p, splits);
     if (w.bytes > 0 && (!workspace || workspace_bytes < w.bytes)) return PCPA_ERR_WORKSPACE;
     uint8_t* const ws = (uint8_t*)workspace;
@@ -226,16 +229,15 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
         g.group_rows = a.group_rows;
         g.local_q = a.local_q;
         g.num_q_heads = a.num_q_heads;
+        g.num_kv_heads = a.num_kv_heads;
         g.group = a.group;
-        g.row_tiles = (a.rows_per_head + kRowsPerGroup - 1) / kRowsPerGroup;
-        g.tiles_total = w.tiles_total;
         g.max_sparse = w.guard_slots;
         int32_t* const plan = (int32_t*)(ws + w.plan);
         hipLaunchKernelGGL(guard_plan_kernel, dim3(1), dim3(kGuardPlanThreads), 0, stream, (const uint8_t*)flags, g,
                            plan);
         if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
         FwdArgs b = history_args(p, q, kv_pages, block_table, page_valid_len, out, lse);
-        b.row_tiles = g.row_tiles;
+        b.row_tiles = (a.rows_per_head + kRowsPerGroup - 1) / kRowsPerGroup;
         b.guard_plan = plan;
         b.splits = w.guard_splits;
         b.guard_slots = w.guard_slots;
@@ -243,7 +245,7 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
         b.part_lse = (float*)(ws + w.gpart_lse);
         void* bargs[] = {&b};
         const int sparse_items = w.guard_slots * w.guard_splits;
-        const int grid = sparse_items > w.tiles_total ? sparse_items : w.tiles_total;
+        const int grid = sparse_items > w.groups_total ? sparse_items : w.groups_total;
         const void* fix = nullptr;
         switch (p->head_dim) {
             case 64: fix = (const void*)history_fwd_kernel<64, true, false, false, false, true>; break;

@@ -350,11 +350,11 @@ __device__ __forceinline__ void tile_step(const FwdArgs& a, const TileCursor& cu
 // and writes a normalised FP32 partial output and log-sum-exp (merged by
 // merge_splits_kernel).
 // FIXUP: the BF16-MFMA pass of a precision-guarded launch.  The plan
-// (guard_plan_kernel) lists the 128-row tiles holding a row the e4m3 pass
-// flagged; in sparse mode workgroup b takes listed tile b / splits and walks
-// history range b % splits into the guard partials (merged by
-// guard_merge_kernel), in dense mode it takes listed tile b and writes the
-// output directly; unlisted workgroups exit at once.
+// (guard_plan_kernel) gathers the rows the e4m3 pass flagged into groups of
+// 128 rows of one KV head; in sparse mode workgroup b takes group b / splits
+// and walks history range b % splits into the guard partials (merged by
+// guard_merge_kernel), in dense mode it takes group b and writes the output
+// directly; workgroups past the plan exit at once.
 template <int D, bool STORE8, bool FP8, bool CAUSAL = false, bool SPLIT = false, bool FIXUP = false>
 __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_fwd_kernel(FwdArgs a) {
     static_assert(!(CAUSAL && SPLIT), "the current-token step is not split");
@@ -391,9 +391,10 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
             if (mode != kGuardDense || (int)blockIdx.x >= listed) return;
             slot = blockIdx.x;
         }
-        const int tile_id = a.guard_plan[kGuardPlanHeader + slot];
-        head = tile_id / a.row_tiles;
-        row_tile = tile_id - head * a.row_tiles;
+        // the KV head whose segment of the plan holds this group
+        head = 0;
+        while (a.guard_plan[2 + head + 1] <= slot) ++head;
+        row_tile = 0;
     } else if constexpr (CAUSAL) {
         const int item = blockIdx.x;
         if (item >= items) return;
@@ -430,9 +431,14 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
     const int gl = lane & 15;
 
     // ---- this lane's query row -------------------------------------------
-    const int row = row_tile * kRowsPerGroup + wave * kRowsPerWave + j;
-    const bool row_ok = row < a.rows_per_head;
-    const int rowc = row_ok ? row : a.rows_per_head - 1;
+    // (FIXUP: the plan's gathered row of the head, -1 for padding)
+    int row;
+    if constexpr (FIXUP)
+        row = a.guard_plan[guard_list_offset(a.num_kv_heads) + slot * kRowsPerGroup + wave * kRowsPerWave + j];
+    else
+        row = row_tile * kRowsPerGroup + wave * kRowsPerWave + j;
+    const bool row_ok = FIXUP ? row >= 0 : row < a.rows_per_head;
+    const int rowc = row_ok ? row : (FIXUP ? 0 : a.rows_per_head - 1);
     const int rank = rowc / a.group_rows;
     const int rem = rowc - rank * a.group_rows;
     const int head_in_group = rem / a.local_q;
