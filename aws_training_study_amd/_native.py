@@ -30,6 +30,7 @@ STATUS_NAMES = {
     -8: "PCPA_ERR_TOO_LARGE",
     -9: "PCPA_ERR_BAD_SCALE",
     -10: "PCPA_ERR_WORKSPACE",
+    -11: "PCPA_ERR_SCRATCH",
 }
 
 DTYPE_BF16 = 1
@@ -44,6 +45,8 @@ FLAG_TABLE_INT64 = 8
 GUARD_MIN_MASS = 384.0
 
 MAX_SPLITS = 64
+# Device scratch of pcpa_history_attention_noalloc, per GPU (bytes).
+NOALLOC_SCRATCH_BYTES = 128 << 20
 
 # Every symbol the header declares; the CPU test suite checks they resolve.
 EXPORTED_SYMBOLS = (
@@ -53,6 +56,7 @@ EXPORTED_SYMBOLS = (
     "pcpa_history_attention",
     "pcpa_history_attention_lse",
     "pcpa_history_attention_split",
+    "pcpa_history_attention_noalloc",
     "pcpa_split_workspace_bytes",
     "pcpa_current_attention",
     "pcpa_kv_cache_write",
@@ -136,6 +140,8 @@ def load_library() -> ctypes.CDLL:
     lib.pcpa_history_attention_split.restype = ctypes.c_int32
     lib.pcpa_history_attention_split.argtypes = (
         [ctypes.POINTER(PcpaParams), ctypes.c_int32] + [ctypes.c_void_p] * 7 + [ctypes.c_int64, ctypes.c_void_p])
+    lib.pcpa_history_attention_noalloc.restype = ctypes.c_int32
+    lib.pcpa_history_attention_noalloc.argtypes = [ctypes.POINTER(PcpaParams), ctypes.c_int32] + [ctypes.c_void_p] * 7
     lib.pcpa_current_attention.restype = ctypes.c_int32
     lib.pcpa_current_attention.argtypes = [ctypes.POINTER(PcpaParams), ctypes.c_int32] + [ctypes.c_void_p] * 7
     lib.pcpa_kv_cache_write.restype = ctypes.c_int32

@@ -50,6 +50,8 @@
 #include "paging_kernels.hpp"
 #include "tile_kernel.hpp"
 
+#include <mutex>
+
 namespace pcpa {
 
 // Launch arguments shared by every attention entry point (Q rows, output).
@@ -264,6 +266,32 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
     return PCPA_OK;
 }
 
+// Scratch of pcpa_history_attention_noalloc: the split partials and guard
+// buffers of a launch, in device memory the library owns instead of a
+// caller workspace.  One copy per GPU, held until the process ends; every
+// call on a GPU shares it (calls that overlap on one GPU race).
+static __device__ __align__(256) uint8_t scratch[PCPA_NOALLOC_SCRATCH_BYTES];
+
+// Device address of `scratch` on each GPU (the array's name is a host-side
+// stand-in, not a device address), looked up once per device with that
+// device current.
+constexpr int kMaxDevices = 64;
+static void* scratch_ptr[kMaxDevices];
+static std::mutex scratch_mutex;
+
+inline int32_t scratch_for_current_device(void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return PCPA_ERR_LAUNCH;
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (!scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return PCPA_ERR_LAUNCH;
+        scratch_ptr[dev] = ptr;
+    }
+    *out = scratch_ptr[dev];
+    return PCPA_OK;
+}
+
 }  // namespace pcpa
 
 extern "C" {
@@ -283,6 +311,7 @@ const char* pcpa_status_string(int32_t status) {
         case PCPA_ERR_TOO_LARGE: return "sizes overflow the kernel's index arithmetic";
         case PCPA_ERR_BAD_SCALE: return "scales must be finite and positive";
         case PCPA_ERR_WORKSPACE: return "workspace missing or smaller than pcpa_split_workspace_bytes";
+        case PCPA_ERR_SCRATCH: return "launch needs more than the library's PCPA_NOALLOC_SCRATCH_BYTES of scratch";
         default: return "unknown status";
     }
 }
@@ -333,6 +362,21 @@ int32_t pcpa_history_attention_split(const pcpa_params* p, int32_t splits, const
                                      float* lse, void* workspace, int64_t workspace_bytes, void* stream) {
     return pcpa::history_launch(p, splits, q, kv_pages, block_table, page_valid_len, out, lse, workspace,
                                 workspace_bytes, (hipStream_t)stream);
+}
+
+int32_t pcpa_history_attention_noalloc(const pcpa_params* p, int32_t splits, const void* q, const void* kv_pages,
+                                       const void* block_table, const int32_t* page_valid_len, void* out, float* lse,
+                                       void* stream) {
+    const int64_t need = pcpa_split_workspace_bytes(p, splits);
+    if (need < 0) return (int32_t)need;
+    if (need > PCPA_NOALLOC_SCRATCH_BYTES) return PCPA_ERR_SCRATCH;
+    void* ws = nullptr;
+    if (need > 0) {
+        const int32_t st = pcpa::scratch_for_current_device(&ws);
+        if (st != PCPA_OK) return st;
+    }
+    return pcpa::history_launch(p, splits, q, kv_pages, block_table, page_valid_len, out, lse, ws, need,
+                                (hipStream_t)stream);
 }
 
 int32_t pcpa_history_attention(const pcpa_params* p, const void* q, const void* kv_pages,

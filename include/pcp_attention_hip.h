@@ -41,6 +41,7 @@ extern "C" {
 #define PCPA_ERR_TOO_LARGE (-8)     /* an index would overflow 32/64-bit maths */
 #define PCPA_ERR_BAD_SCALE (-9)     /* a scale is not finite and positive    */
 #define PCPA_ERR_WORKSPACE (-10)    /* workspace missing or too small        */
+#define PCPA_ERR_SCRATCH (-11)      /* more than PCPA_NOALLOC_SCRATCH_BYTES   */
 
 /* params.flags bits. */
 /* Run both GEMMs as BF16 MFMAs even for an e4m3 cache: K/V are widened to
@@ -187,6 +188,25 @@ int32_t pcpa_history_attention_split(const pcpa_params* params, int32_t splits, 
                                      const void* kv_pages, const void* block_table,
                                      const int32_t* page_valid_len, void* out, float* lse,
                                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * pcpa_history_attention_split with no workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The split partials and guard
+ * buffers live in a fixed array of PCPA_NOALLOC_SCRATCH_BYTES that the
+ * library holds on every GPU it runs on until the process ends; this entry
+ * point calls no hipMalloc, hipFree or allocating routine.  A launch whose
+ * pcpa_split_workspace_bytes(params, splits) exceeds the array returns
+ * PCPA_ERR_SCRATCH.  The array needs no initialisation and keeps the last
+ * call's contents; every call on one GPU shares it, so calls that overlap
+ * on one GPU (several streams or host threads) race and must be ordered by
+ * the caller.  No counterpart in the reference (its kernel allocates its
+ * output in device memory, kernel.py:124).
+ */
+#define PCPA_NOALLOC_SCRATCH_BYTES (128ll << 20)
+int32_t pcpa_history_attention_noalloc(const pcpa_params* params, int32_t splits, const void* q,
+                                       const void* kv_pages, const void* block_table,
+                                       const int32_t* page_valid_len, void* out, float* lse, void* stream);
 
 /*
  * Causal attention of the current tokens among themselves, optionally merged
