@@ -549,6 +549,7 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     const int64_t q_off = query_row_offset<D>(a, q_row, head);
     const uint8_t* const qrow = a.q + q_off;
 
+
     v8i q[QK];
     SoftmaxRow sm;
     {
@@ -643,14 +644,21 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     }
 
     // ---- epilogue: O = O^T / l, bf16; log-sum-exp ---------------------------
-    // The row again, from the lane id: kept live through the walk its offset
-    // takes registers there (the plain and log-sum-exp instantiations then
-    // spill; the split ones keep it).
-    const int row = SPLIT ? q_row
-                          : row_tile * kRowsPerGroup + wave * 32 +
-                                (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) & 31);
+    // The row, its offset and the lane half again, from an opaque lane id and
+    // opaque divisors: values kept live through the walk (the row offset, the
+    // reciprocals of the row maps' divisors, lane-derived store offsets) take
+    // registers there and spill (outside the loop).  The split
+    // instantiations keep the row and its offset from the prologue instead:
+    // at their register pressure every recomputation tried moved a Q
+    // fragment's spill into the loop.
+    int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    asm volatile("" : "+v"(lane_e));
+    const int he = SPLIT ? h : lane_e >> 5;
+    FwdArgs ag = a;
+    asm volatile("" : "+s"(ag.group_rows), "+s"(ag.local_q));
+    const int row = SPLIT ? q_row : row_tile * kRowsPerGroup + wave * 32 + (lane_e & 31);
     const bool row_ok = row < a.rows_per_head;
-    const int64_t row_off = SPLIT ? q_off : query_row_offset<D>(a, row, head);
+    const int64_t row_off = SPLIT ? q_off : query_row_offset<D>(ag, row, head);
     const float scale = sm.l > 0.f ? a.v_scale / sm.l : 0.f;
     // sum_k exp(score_k) = l * 2^(m - 6), less the average overestimate of
     // the linear-mantissa exp2

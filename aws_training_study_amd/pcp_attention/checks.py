@@ -14,6 +14,8 @@ from .workloads import PagedProblem
 
 def dequantised_history(problem: PagedProblem, device) -> tuple[torch.Tensor, torch.Tensor]:
     inputs = problem.inputs
+    if inputs.k is None:
+        raise ValueError("a problem built from per-rank local inputs has no global history to check against")
     k = inputs.k.to(device).float() * inputs.k_scale
     v = inputs.v.to(device).float() * inputs.v_scale
     return k, v

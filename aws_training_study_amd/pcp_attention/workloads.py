@@ -28,7 +28,7 @@ from dataclasses import dataclass, replace
 import torch
 
 from .config import PCPAttentionConfig
-from .inputs import HistoryInputs, make_scaled_inputs
+from .inputs import HistoryInputs, make_local_inputs, make_scaled_inputs
 from .layout import shard_history, shard_history_bucket, stacked_query
 from .paging import make_block_table, pack_page_pool, page_valid_lengths
 
@@ -157,3 +157,30 @@ def build_workload_problem(workload: Workload | str, seed: int) -> PagedProblem:
         workload = get_workload(workload)
     config = workload.resolve(seed)
     return build_paged_problem(config, seed, kv_scale=workload.kv_scale, k_prescale=workload.k_prescale)
+
+
+def build_local_problem(config: PCPAttentionConfig, seed: int, *, shuffle_pages: bool = True) -> PagedProblem:
+    """The memory-safe per-rank inputs of the reference's unchecked runs.
+
+    Every rank draws only its own Q shard and local cache with seed
+    ``seed + 104729 * rank`` (``make_local_inputs``, run_poc.py:107-134),
+    the cache padded with zero blocks to ``max_local_blocks`` and valid up to
+    ``actual_local_history_len`` per rank, as the reference's runner does
+    (run_poc.py:221-237).  No global tensor exists: ``inputs`` carries only
+    the (unit) scales, and the problem has no dense reference.
+    """
+    if not config.is_history_aligned:
+        raise ValueError("per-rank local inputs need a history that is a multiple of pcp_size * interleave_size")
+    q_shards, k_shards, v_shards = [], [], []
+    for rank in range(config.pcp_size):
+        q, k, v = make_local_inputs(config, seed, rank)
+        q_shards.append(q)
+        k_shards.append(k)
+        v_shards.append(v)
+    if shuffle_pages:
+        table = make_block_table(config, seed + 1)
+    else:
+        table = torch.arange(config.num_pages, dtype=torch.int32).reshape(config.pcp_size, config.max_local_blocks)
+    pool = pack_page_pool(k_shards, v_shards, config, table)
+    inputs = HistoryInputs(config, None, None, None, 1.0, 1.0)
+    return PagedProblem(config, inputs, torch.stack(q_shards), pool, table, page_valid_lengths(config))

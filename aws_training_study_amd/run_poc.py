@@ -76,7 +76,7 @@ def run_hip(cfg: PCPAttentionConfig, seed: int, check: str, kv_scale: str, itera
 
     from .pcp_attention.checks import dense_reference
     from .pcp_attention.kernel import make_history_attention_kernel
-    from .pcp_attention.workloads import build_paged_problem
+    from .pcp_attention.workloads import build_local_problem, build_paged_problem
 
     if iterations < 0 or warmups < 0:
         raise ValueError("benchmark iterations and warmups must be non-negative")
@@ -85,7 +85,12 @@ def run_hip(cfg: PCPAttentionConfig, seed: int, check: str, kv_scale: str, itera
     if not torch.cuda.is_available():
         raise RuntimeError("--backend hip needs a visible MI355X GPU")
     device = torch.device("cuda", 0)
-    problem = build_paged_problem(cfg, seed, kv_scale=kv_scale if cfg.kv_dtype == "fp8_e4m3fn" else "none")
+    if check == "none":
+        # as the reference's unchecked runs (run_poc.py:221-222): every rank's
+        # own seeded Q shard and local cache only, no global tensors
+        problem = build_local_problem(cfg, seed)
+    else:
+        problem = build_paged_problem(cfg, seed, kv_scale=kv_scale if cfg.kv_dtype == "fp8_e4m3fn" else "none")
     gpu = problem.to(device)
     kernel = make_history_attention_kernel(cfg)
 
@@ -111,32 +116,41 @@ def run_hip(cfg: PCPAttentionConfig, seed: int, check: str, kv_scale: str, itera
         print("HIP run completed", flush=True)
 
     if iterations:
+        # The reference's timing (run_poc.py:279-327): a host clock around
+        # each call and its completion (a one-element device-to-host copy).
         for _ in range(warmups):
-            invoke(out)
+            invoke(out).reshape(-1)[:1].cpu()
         torch.cuda.synchronize()
-        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iterations)]
         host_ms = []
-        for begin, end in events:
+        for _ in range(iterations):
             start = time.perf_counter()
-            begin.record()
-            invoke(out)
-            end.record()
-            end.synchronize()
+            marker = invoke(out).reshape(-1)[:1].cpu()
             host_ms.append((time.perf_counter() - start) * 1e3)
-        device_ms = [b.elapsed_time(e) for b, e in events]
+            _ = marker[0].item()
+        # Device time: the same calls back to back between one pair of HIP
+        # events (an event pair per call would add queue work to each).
+        stream = torch.cuda.current_stream(device)
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        begin.record(stream)
+        for _ in range(iterations):
+            invoke(out)
+        end.record(stream)
+        end.synchronize()
+        device_ms = begin.elapsed_time(end) / iterations
         ordered = sorted(host_ms)
         p90 = ordered[max(0, (9 * len(ordered) + 9) // 10 - 1)]
         flops = 4.0 * cfg.num_q_heads * cfg.current_len * cfg.actual_history_len * cfg.head_dim
-        peak = 5000.0 if cfg.kv_dtype == "fp8_e4m3fn" else 2500.0
-        median_dev = statistics.median(device_ms)
+        fp8 = not kernel.uses_bf16_mfma()
+        peak = 5000.0 if fp8 else 2500.0
+        mean_ms = statistics.fmean(host_ms)
         print(
             "benchmark: mode=single_launch_all_ranks, "
             f"kv_dtype={cfg.kv_dtype}, iterations={iterations}, warmups={warmups}, "
             f"min_ms={min(host_ms):.3f}, median_ms={statistics.median(host_ms):.3f}, "
-            f"mean_ms={statistics.fmean(host_ms):.3f}, p90_ms={p90:.3f}, max_ms={max(host_ms):.3f}, "
-            f"device_median_ms={median_dev:.3f}, tflops={flops / median_dev / 1e9:.1f}, "
-            f"pct_mfma_peak={100 * flops / median_dev / 1e9 / peak:.2f}, "
-            f"global_current_tokens_per_s={cfg.current_len / (statistics.fmean(host_ms) / 1e3):.1f}",
+            f"mean_ms={mean_ms:.3f}, p90_ms={p90:.3f}, max_ms={max(host_ms):.3f}, "
+            f"device_mean_ms={device_ms:.3f}, tflops={flops / device_ms / 1e9:.1f}, "
+            f"pct_mfma_peak={100 * flops / device_ms / 1e9 / peak:.2f}, "
+            f"global_current_tokens_per_s={cfg.current_len / (mean_ms / 1e3):.1f}",
             flush=True,
         )
 

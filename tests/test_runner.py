@@ -72,3 +72,42 @@ def test_run_poc_cpu_backend_points_to_oracle():
 def test_run_poc_args():
     args = parse_args(["--backend", "hip", "--preset", "full", "--start-offset", "65536", "--kv-dtype", "fp8_e4m3fn"])
     assert args.actual_history_len == 65536 and args.backend == "hip"
+
+
+def test_local_problem_is_the_per_rank_draws_packed_into_pages():
+    """--check none inputs: rank r's own seeded Q shard and local cache
+    (seed + 104729 * r, run_poc.py:107-134), padded to max_local_blocks with
+    zero pages (run_poc.py:231-237) and placed by the block table."""
+    from aws_training_study_amd.pcp_attention.kernel import pack_local_kv
+    from aws_training_study_amd.pcp_attention.workloads import build_local_problem
+
+    cfg = get_preset("tiny").with_overrides(backend="hip", max_history_len=4096, actual_history_len=2048)
+    problem = build_local_problem(cfg, seed=9)
+    assert cfg.actual_local_blocks == 1 and cfg.max_local_blocks == 2
+    table = problem.block_table
+    for rank in range(cfg.pcp_size):
+        q, k, v = make_local_inputs(cfg, seed=9, rank=rank)
+        assert torch.equal(problem.q_stacked[rank], q)
+        assert torch.equal(problem.kv_pages[int(table[rank, 0])].view(torch.uint8),
+                           pack_local_kv(k, v)[0].view(torch.uint8))
+        assert not bool(problem.kv_pages[int(table[rank, 1])].view(torch.uint8).any())
+    # every rank's 512 valid tokens in its first block, none in the padding
+    assert problem.page_valid_len.tolist() == [[512, 0]] * cfg.pcp_size
+    assert problem.k_scale == problem.v_scale == 1.0
+    # the oracle over those pages is ordinary attention over every rank's cache
+    shape = orc.OracleShape.from_config(cfg)
+    pool = orc.decode_e4m3fn(problem.kv_pages.view(torch.uint8).numpy())
+    q = orc.decode_bfloat16(problem.q_stacked.view(torch.int16).numpy().view(np.uint16))
+    out = orc.paged_history_attention(q, pool, table.numpy(), problem.page_valid_len.numpy(), shape)
+    keys = np.concatenate([pool[int(table[r, 0])].reshape(2, 2, 512, 256)[0] for r in range(4)], axis=1)
+    vals = np.concatenate([pool[int(table[r, 0])].reshape(2, 2, 512, 256)[1] for r in range(4)], axis=1)
+    want = orc.dense_history_attention(q[1], keys, vals, shape.softmax_scale)
+    np.testing.assert_allclose(out[1], want, rtol=0, atol=1e-12)
+
+
+def test_local_problem_needs_an_aligned_history():
+    from aws_training_study_amd.pcp_attention.workloads import build_local_problem
+
+    cfg = get_preset("tiny").with_overrides(backend="hip", actual_history_len=1000)
+    with pytest.raises(ValueError, match="multiple of pcp_size"):
+        build_local_problem(cfg, seed=1)
