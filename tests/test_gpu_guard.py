@@ -55,8 +55,9 @@ def _sample(cfg, count, seed):
     return np.concatenate([corners, rows])
 
 
-def _paged_reference(problem, q_stacked, rows, page_valid_len):
-    """float64 attention of the listed rows over exactly the pages' valid prefixes."""
+def _paged_reference(problem, q_stacked, rows, page_valid_len, with_lse=False):
+    """float64 attention of the listed rows over exactly the pages' valid
+    prefixes (and each row's natural-log sum of exp(score))."""
     cfg = problem.config
     pool = orc.decode_e4m3fn(problem.kv_pages.view(torch.uint8).numpy()).reshape(
         -1, 2, cfg.num_kv_heads, cfg.block_size, cfg.head_dim)
@@ -74,11 +75,12 @@ def _paged_reference(problem, q_stacked, rows, page_valid_len):
     q = orc.decode_bfloat16(q_stacked.view(torch.int16).numpy().view(np.uint16))
     group = cfg.num_q_heads // cfg.num_kv_heads
     out = np.empty((len(rows), cfg.head_dim))
+    lse = np.empty(len(rows))
     for i, (rank, qh, tok) in enumerate(rows):
         g = qh // group
-        out[i] = orc.dense_history_attention(q[rank, qh, tok][None, None, :], k[g:g + 1], v[g:g + 1],
-                                             cfg.softmax_scale)[0, 0]
-    return out
+        o, l = orc.attention_with_lse(q[rank, qh, tok][None, None, :], k[g:g + 1], v[g:g + 1], cfg.softmax_scale)
+        out[i], lse[i] = o[0, 0], l[0, 0]
+    return (out, lse) if with_lse else out
 
 
 def _model(problem, q_stacked, rows, page_valid_len, kernel="overlap", exp2="fast", **kw):
@@ -205,6 +207,52 @@ def _peaked_case(cfg, k_prescale, q_factor, exp2, device, rows):
           f"{(mass < _native.GUARD_MIN_MASS).mean():.2f}", flush=True)
     _check_model(_pick(fp8, sample), model, mass, f"{label} fp8")
     _check_bar(_pick(auto, sample), ref, f"{label} auto")
+
+
+# ---- the e4m3 log-sum-exp (the prefill merge's weights)
+
+
+@pytest.mark.parametrize("q_factor,exp2,splits", [(1, "fast", 1), (1, "exact", 2), (2, "fast", 2), (2, "exact", 1)])
+def test_fp8_lse_matches_model_and_auto_lse_meets_the_bar(q_factor, exp2, splits, cuda_device):
+    """``precision="fp8"``: the lse equals the model's (which applies the same
+    linear-mantissa bias correction, 0.03987 in ln) to fp32 noise plus the odd
+    P code rounded the other way, on rows of mass >= 64.  ``"auto"``: rows
+    whose mass is below the guard threshold - where the bias, a mean over
+    evenly spread exponents, does not hold - carry the BF16 fixup's exact lse;
+    every row is within 3e-2 (max) / 3e-3 (mean) of the float64 lse.  The
+    residue is Q's rounding to e4m3, which grows with the scores: the model
+    with exact Q is within 1.2e-3 of float64 at Q x1, with e4m3 Q 9.4e-3
+    (x1) and 2.1e-2 (x2, rows above the guard mass)."""
+    cfg = FOUR
+    problem = _problem(cfg, "none", 47)
+    q = _scaled_q(problem, q_factor)
+    label = f"lse Q x{q_factor} exp2 {exp2} splits {splits}"
+    print(f"case {label}", flush=True)
+    gpu = problem.to(cuda_device)
+    qd = q.to(cuda_device)
+    kernel = make_history_attention_kernel(cfg)
+    kw = dict(page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale, v_scale=problem.v_scale, exp2=exp2,
+              return_lse=True)
+    _, lse8 = kernel(qd, gpu.kv_pages, gpu.block_table, precision="fp8", splits=splits, **kw)
+    auto_out, lse_auto = kernel(qd, gpu.kv_pages, gpu.block_table, **kw)
+    torch.cuda.synchronize()
+    sample = _sample(cfg, 192, 47 + q_factor)
+    _, model_lse, mass = _model(problem, q, sample, problem.page_valid_len, exp2=exp2, splits=splits,
+                                return_mass=True)
+    ref_out, ref_lse = _paged_reference(problem, q, sample, problem.page_valid_len, with_lse=True)
+    got8 = np.array([float(lse8[r, h, t]) for r, h, t in sample])
+    got_auto = np.array([float(lse_auto[r, h, t]) for r, h, t in sample])
+    ok = mass >= 64
+    diff = np.abs(got8 - model_lse)
+    err8 = np.abs(got8 - ref_lse)
+    err_auto = np.abs(got_auto - ref_lse)
+    print(f"{label}: fp8 vs model on {ok.sum()} of {len(ok)} rows max={diff[ok].max(initial=0):.3e} "
+          f"mean={diff[ok].mean() if ok.any() else 0:.3e}; fp8 vs float64 max={err8.max():.3e} "
+          f"mean={err8.mean():.3e}; auto vs float64 max={err_auto.max():.3e} mean={err_auto.mean():.3e}", flush=True)
+    if ok.any():
+        assert diff[ok].max() <= 2e-3 and diff[ok].mean() <= 2e-4, label
+    assert err_auto.max() <= 3e-2 and err_auto.mean() <= 3e-3, label
+    _check_bar(_pick(auto_out, sample), ref_out, f"{label} auto output")
 
 
 # ---- the tile kernel's e4m3 path (head_dim 64 / 128) against the model
