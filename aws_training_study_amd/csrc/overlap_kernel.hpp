@@ -166,6 +166,7 @@ struct Lanes {
     uint32_t v_addr;  // PV operand, V stage 0, d tile 0 (includes the ring offset)
     uint32_t dma_k;   // byte offset of the lane's K chunk of DMA block `wave` in a tile
     uint32_t dma_v;   // same for V (its own swizzle)
+    int rsel;         // row-sum selector operand word (see s_half)
 };
 
 __device__ __forceinline__ bool is_real(const FwdArgs& a, const TileCursor& c) {
@@ -329,17 +330,24 @@ __device__ __forceinline__ void load_v(const FwdArgs& a, const TileCursor& c, ui
 // starts the first V-operand read of the PV half that follows (stage VST).
 // Also adds to l the row sum of P_last, the probabilities the preceding PV
 // half consumed, scaled by the alpha that PV half applied.
+//
+// The row sum is one 16x16x128 MFMA (half the cycles of a 32x32x64 one):
+// read as its B operand, P_last's lane 16g + j holds K group g of column j,
+// i.e. keys of query row 16 (g & 1) + j (g >> 1 picks the key half).  The
+// selector A operand (lane 16g + i holds row i, K group g) is e4m3 1.0 where
+// ((i >> 2) & 1) == (g & 1), else 0, so output row i of column j sums the
+// groups of row 16 ((i >> 2) & 1) + j over both key halves.  Output lane l
+// holds rows 4 (l >> 4) + v of column l & 15: the sum of query row l & 31,
+// the row that lane holds in every other operand.
 template <int D, int KST, bool PREFETCH_V, int VST>
 __device__ __forceinline__ void s_half(uint32_t k_addr, uint32_t v_addr, const v8i (&q)[Shape<D>::QK], v16f (&s)[2],
-                                       v2i (&xv)[4], const v8i& p_last, SoftmaxRow& sm) {
+                                       v2i (&xv)[4], const v8i& p_last, SoftmaxRow& sm, int rsel) {
     using S = Shape<D>;
-    // ones (e4m3 1.0) x P_last puts sum_k P_last[k][q] in every accumulator
-    // of query column q.  The ones operand is rebuilt from an opaque register
-    // instead of occupying 8 VGPRs for good.
-    int one = 0x38383838;
-    asm volatile("" : "+v"(one));
-    const v8i ones = {one, one, one, one, one, one, one, one};
-    v16f rowsum = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, p_last, v16f{}, 0, 0, 0, 0, 0, 0);
+    // The selector operand is rebuilt from an opaque register instead of
+    // occupying 8 VGPRs for good.
+    asm volatile("" : "+v"(rsel));
+    const v8i sel = {rsel, rsel, rsel, rsel, rsel, rsel, rsel, rsel};
+    v4f rowsum = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(sel, p_last, v4f{}, 0, 0, 0, 0, 0, 0);
     v4i kr[2][2];
     auto issue_k = [&](auto oc) {
         constexpr int op = decltype(oc)::value, c = op >> 1, t = op & 1;
@@ -365,7 +373,7 @@ __device__ __forceinline__ void s_half(uint32_t k_addr, uint32_t v_addr, const v
         const v8i kop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         s[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kop, q[c], c == 0 ? v16f{} : s[t], 0, 0, 0, 0, 0, 0);
     });
-    // All 16 row-sum registers stay allocated until here: the inline-asm LDS
+    // All 4 row-sum registers stay allocated until here: the inline-asm LDS
     // reads above are invisible to the hazard checks and must not be given
     // registers that the in-flight MFMA is still going to write.
     asm volatile("" : "+v"(rowsum));
@@ -454,7 +462,7 @@ __device__ __forceinline__ void iteration(const FwdArgs& a, uint8_t* lds, int wa
     if constexpr (!LATE) {
         // S(j), then PV(j-1) beside softmax(j)
         constexpr int VST = (J4 + 3) % kStages;
-        s_half<D, KST, true, VST>(k_addr, v_addr, q, s, xv, pbuf[J4 & 1], sm);
+        s_half<D, KST, true, VST>(k_addr, v_addr, q, s, xv, pbuf[J4 & 1], sm, L.rsel);
         pv_half<D, VST, true, FAST>(v_addr, xv, o, pbuf[(J4 + 1) & 1], s, pbuf[J4 & 1], sm,
                               cs.k0, h);
     } else {
@@ -462,7 +470,7 @@ __device__ __forceinline__ void iteration(const FwdArgs& a, uint8_t* lds, int wa
         constexpr int VST = (J4 + 2) % kStages;
         pv_half<D, VST, false, FAST>(v_addr, xv, o, pbuf[J4 & 1], s, pbuf[(J4 + 1) & 1], sm,
                                cs.km1, h);
-        s_half<D, KST, false, 0>(k_addr, v_addr, q, s, xv, pbuf[J4 & 1], sm);
+        s_half<D, KST, false, 0>(k_addr, v_addr, q, s, xv, pbuf[J4 & 1], sm, L.rsel);
     }
 
     cs.km1 = cs.k0;
@@ -609,6 +617,7 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
         const int key = lds_row<true>(drow);
         L.dma_k = key * ROW + (pos ^ chunk_swizzle<true, CHUNKS>(drow)) * 16;
         L.dma_v = key * ROW + (pos ^ chunk_swizzle_v<true, CHUNKS>(drow)) * 16;
+        L.rsel = ((lane ^ (lane >> 2)) & 4) ? 0 : 0x38383838;
     }
 
     v16f o[DT];

@@ -143,6 +143,7 @@ class HistoryAttentionKernel:
         # bound): launch parameters and split counts are cached
         self._call_params = {}
         self._splits = {}
+        self._ws_sizes = {}
 
     def _params(self, num_pages: int, k_scale: float, v_scale: float):
         return self._native.PcpaParams(
@@ -379,13 +380,17 @@ class HistoryAttentionKernel:
 
     def workspace_bytes(self, n_split: int, precision: str = "auto") -> int:
         """Bytes of the workspace of a call with ``n_split`` splits and ``precision``."""
-        params = self._params(self.config.num_pages, 1.0, 1.0)
-        if self.guarded(precision):
-            params.flags |= self._native.FLAG_PRECISION_GUARD
-        size = self._lib.pcpa_split_workspace_bytes(ctypes.byref(params), n_split)
-        if size < 0:
-            self._native.check(int(size))
-        return int(size)
+        key = (int(n_split), self.guarded(precision))
+        size = self._ws_sizes.get(key)
+        if size is None:
+            params = self._params(self.config.num_pages, 1.0, 1.0)
+            if key[1]:
+                params.flags |= self._native.FLAG_PRECISION_GUARD
+            size = self._lib.pcpa_split_workspace_bytes(ctypes.byref(params), key[0])
+            if size < 0:
+                self._native.check(int(size))
+            size = self._ws_sizes[key] = int(size)
+        return size
 
     def split_workspace_bytes(self, n_split: int) -> int:
         """Bytes of the split partials of a call with ``n_split`` splits (no guard)."""
