@@ -179,15 +179,21 @@ __global__ void __launch_bounds__(kGuardPlanThreads) guard_plan_kernel(const uin
     }
 }
 
-// Sparse mode: one thread per (slot row, 8 consecutive d) merges the splits'
-// partials of a listed row by log-sum-exp (as merge_splits_kernel) into out
-// (bf16) and lse.  Other modes, padding and slots past the list: nothing.
-__global__ void __launch_bounds__(256) guard_merge_kernel(const float* part_o, const float* part_lse, int splits,
-                                                          const int32_t* plan, GuardShape g, int d_vec8, uint8_t* out,
-                                                          float* lse_out) {
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// Sparse mode: one workgroup per slot row merges the splits' partials of a
+// listed row by log-sum-exp (as merge_splits_kernel) into out (bf16) and
+// lse.  Thread t takes 8 consecutive d (t % d_vec8) of the ranges t /
+// d_vec8, t / d_vec8 + groups, ...; the groups' sums meet in LDS, so the
+// dependent loads per thread are splits / groups rather than splits.
+// Other modes, padding and slots past the list: nothing.
+constexpr int kGuardMergeThreads = 256;
+
+__global__ void __launch_bounds__(kGuardMergeThreads) guard_merge_kernel(const float* part_o, const float* part_lse,
+                                                                         int splits, const int32_t* plan, GuardShape g,
+                                                                         int d_vec8, uint8_t* out, float* lse_out) {
+    __shared__ float red[kGuardMergeThreads * 8];
+    __shared__ float wred[kGuardMergeThreads];
     if (plan[1] != kGuardSparse) return;
-    const int64_t slot_row = idx / d_vec8;
+    const int64_t slot_row = blockIdx.x;
     const int slot = (int)(slot_row / kRowsPerGroup);
     if (slot >= plan[0]) return;
     const int r = plan[guard_list_offset(g.num_kv_heads) + slot_row];
@@ -196,16 +202,19 @@ __global__ void __launch_bounds__(256) guard_merge_kernel(const float* part_o, c
     while (plan[2 + head + 1] <= slot) ++head;
     const int64_t row = guard_row_index(g, head, r);
     const int D = d_vec8 * 8;
-    const int d0 = (int)(idx - slot_row * d_vec8) * 8;
+    const int tid = threadIdx.x;
+    const int groups = kGuardMergeThreads / d_vec8;  // d_vec8 divides 256 (D = 64, 128, 256)
+    const int sg = tid / d_vec8;
+    const int d0 = (tid - sg * d_vec8) * 8;
     const int64_t stride = (int64_t)g.max_sparse * kRowsPerGroup;  // rows of one split's partials
-    // (unrolled so that several ranges' loads are in flight together)
+    // every thread finds the largest range lse (few loads, all in flight)
     float mx = -INFINITY;
 #pragma unroll 8
     for (int sp = 0; sp < splits; ++sp) mx = fmaxf(mx, part_lse[sp * stride + slot_row]);
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float wsum = 0.f;
-#pragma unroll 4
-    for (int sp = 0; sp < splits; ++sp) {
+#pragma unroll 2
+    for (int sp = sg; sp < splits; sp += groups) {
         const float l = part_lse[sp * stride + slot_row];
         const float w = l == -INFINITY ? 0.f : __expf(l - mx);
         wsum += w;
@@ -216,6 +225,17 @@ __global__ void __launch_bounds__(256) guard_merge_kernel(const float* part_o, c
             acc[i] = fmaf(w, lo[i], acc[i]);
             acc[4 + i] = fmaf(w, hi[i], acc[4 + i]);
         }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) red[tid * 8 + i] = acc[i];
+    wred[tid] = wsum;
+    __syncthreads();
+    if (sg != 0) return;
+    for (int o = 1; o < groups; ++o) {
+        const int t = o * d_vec8 + tid;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += red[t * 8 + i];
+        wsum += wred[t];
     }
     const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
     uint32_t wv[4];

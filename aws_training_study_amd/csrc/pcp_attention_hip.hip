@@ -93,13 +93,13 @@ inline WorkspaceLayout workspace_layout(const pcpa_params* p, int splits) {
     if (guarded(p)) {
         // fixup: the flagged rows gathered into groups of 128 (at most as
         // many groups as 128-row tiles); the history's key tiles cut into
-        // ranges of at least 4 (256 keys), at most 64, so that a few flagged
+        // ranges of at least 2 (128 keys), 64 ranges at most, so that a few flagged
         // rows cost a short walk rather than a whole history's
         const int64_t entries = (int64_t)p->pcp_size * p->max_local_blocks;
         const int64_t key_tiles = entries * (p->block_size / kKeyTile);
         const int64_t rows_per_head = rows / p->num_q_heads * (p->num_q_heads / p->num_kv_heads);
         w.groups_total = (int32_t)((rows_per_head + kRowsPerGroup - 1) / kRowsPerGroup * p->num_kv_heads);
-        int64_t gs = key_tiles / 4;
+        int64_t gs = key_tiles / 2;
         gs = gs < 1 ? 1 : gs > 64 ? 64 : gs;
         w.guard_splits = (int32_t)gs;
         const int64_t slots = kGuardPartialRows / kRowsPerGroup / gs;
@@ -257,8 +257,8 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
         }
         if (hipLaunchKernel(fix, dim3(grid), dim3(kThreads), bargs, 0, stream) != hipSuccess) return PCPA_ERR_LAUNCH;
         const int d_vec8 = p->head_dim / 8;
-        const int64_t threads = (int64_t)w.guard_slots * kRowsPerGroup * d_vec8;
-        hipLaunchKernelGGL(guard_merge_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+        const int64_t slot_rows = (int64_t)w.guard_slots * kRowsPerGroup;
+        hipLaunchKernelGGL(guard_merge_kernel, dim3((unsigned)slot_rows), dim3(kGuardMergeThreads), 0, stream,
                            (const float*)b.part_o, (const float*)b.part_lse, w.guard_splits, (const int32_t*)plan, g,
                            d_vec8, (uint8_t*)out, lse);
         if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;

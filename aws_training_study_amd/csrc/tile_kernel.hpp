@@ -50,6 +50,7 @@ struct LaneMap {
     uint32_t v_addr[S::ES == 1 ? 1 : 2];  // PV A operand base(s)
     uint32_t dma_off[S::DMA_SPLIT ? S::DMA_PER_WAVE : 1];   // global byte offset of the lane's K DMA chunk
     uint32_t dma_off_v[S::DMA_SPLIT ? S::DMA_PER_WAVE : 1]; // same for the V tile (its own swizzle)
+    int rsel;  // e4m3 MFMAs: the row-sum selector operand word (e4m3 1.0 bytes or 0)
 };
 
 // Issue asynchronous global->LDS loads of one 64-key K tile and V tile.  The
@@ -224,14 +225,17 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
                 pk = __builtin_amdgcn_cvt_pk_fp8_f32(s[t][4 * q4 + 2], s[t][4 * q4 + 3], pk, true);
                 pop[4 * t + q4] = pk;
             }
-        // ones (e4m3 1.0) x P^T puts sum_k P[k][q] in every accumulator of
-        // query column q, in both lane halves: the sum of exactly the e4m3
-        // probabilities the PV MFMAs weigh V with, so the output weights sum
-        // to one.
-        int one = 0x38383838;
-        asm volatile("" : "+v"(one));
-        const v8i ones = {one, one, one, one, one, one, one, one};
-        v16f rowsum = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, pop, v16f{}, 0, 0, 0, 0, 0, 0);
+        // The row sum of exactly the e4m3 probabilities the PV MFMAs weigh V
+        // with (so the output weights sum to one), by one 16x16x128 MFMA:
+        // read as its B operand, lane 16g + j of P^T holds K group g of
+        // column j, keys of query row 16 (g & 1) + j; the selector A operand
+        // (lane 16g + i: row i, K group g) is e4m3 1.0 where ((i >> 2) & 1)
+        // == (g & 1), so output lane l (rows 4 (l >> 4) + v, column l & 15)
+        // holds the sum of query row l & 31 over both key halves.
+        int rsel = L.rsel;
+        asm volatile("" : "+v"(rsel));
+        const v8i sel = {rsel, rsel, rsel, rsel, rsel, rsel, rsel, rsel};
+        v4f rowsum = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(sel, pop, v4f{}, 0, 0, 0, 0, 0, 0);
         // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1): keys
         // 32*(grp>>1) + [0, 32) of column d, 8 per transposing read; the
         // d tiles are read two at a time, one pair ahead of the MFMAs.
@@ -262,7 +266,7 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
                     __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, pop, st.o[2 * pair + k], 0, 0, 0, 0, 0, 0);
             }
         }
-        // All 16 row-sum registers stay allocated until here: the inline-asm
+        // All 4 row-sum registers stay allocated until here: the inline-asm
         // LDS reads above are invisible to the MFMA hazard checks and must not
         // be given registers the in-flight MFMA is still going to write.
         asm volatile("" : "+v"(rowsum));
@@ -509,6 +513,7 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
         // key 32*(grp>>1) + (gl>>1) (+ 8s for the other reads) -> row below
         const int row = lds_row<FP8>(32 * (grp >> 1) + (gl >> 1));
         L.v_addr[0] = row * ROW + (((grp & 1) ^ chunk_swizzle_v<FP8, CHUNKS>(row)) << 4) + 8 * (gl & 1);
+        L.rsel = ((lane ^ (lane >> 2)) & 4) ? 0 : 0x38383838;
     } else {
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {

@@ -3,10 +3,12 @@ attention among the current tokens, and its log-sum-exp merge with the
 history output, against the float64 oracle.
 
 Bars: outputs max-abs <= 2e-2 and mean-abs <= 2e-3 (as for the history
-attention).  Log-sum-exp (natural log): e4m3 MFMA paths max-abs <= 5e-2,
-mean-abs <= 1e-2 - rounding Q to e4m3 alone moves the lse of the 16-rank
-FP8 workload by up to 1.2e-2 (mean 2.2e-3) against the exact Q; BF16 MFMA
-paths max-abs <= 5e-3, mean-abs <= 5e-4.
+attention).  Log-sum-exp (natural log): e4m3 MFMA paths max-abs <= 3e-2,
+mean-abs <= 5e-3 - rounding Q to e4m3 alone moves the lse of the 16-rank
+FP8 workload by up to 1.2e-2 (mean 2.3e-3) against the exact Q (the e4m3
+kernels' lse is pinned to their numerical model to 2e-3 in
+test_gpu_guard.py); BF16 MFMA paths max-abs <= 1e-4, mean-abs <= 2e-5
+(measured: 2e-6 / 6e-7).
 """
 
 from __future__ import annotations
@@ -29,7 +31,7 @@ from test_gpu_parity import _assert_close, _real_history, _sample_rows
 
 pytestmark = pytest.mark.gpu
 
-LSE_TOL = {"fp8": (5e-2, 1e-2), "bf16": (5e-3, 5e-4)}
+LSE_TOL = {"fp8": (3e-2, 5e-3), "bf16": (1e-4, 2e-5)}
 
 
 def _assert_lse(actual, expected, mode, label):

@@ -6,8 +6,9 @@ Each case draws pcp size, interleave, current tokens per rank, heads, head
 dim, cache dtype, history precision and a runtime history length from a
 fixed seed; ``PCPA_RANDOM_CASES`` widens the sweep as for the history
 kernel's.  Bars as in test_gpu_current.py (outputs 2e-2 / 2e-3; lse by the
-MFMA precision of the history part, e4m3 held to the same short-history
-allowance as test_gpu_random_configs.py when below 2048 history tokens).
+MFMA precision of the history part), on every case: an e4m3 cache is drawn
+with the guarded default, unguarded e4m3 MFMAs (only on histories of 2048
+tokens or more, where no row's softmax rests on a few keys) or BF16 MFMAs.
 """
 
 from __future__ import annotations
@@ -56,7 +57,9 @@ def _draw(i: int):
                                      backend="hip").validate()
         except ValueError:
             continue
-        precision = str(rng.choice(["fp8", "bf16"])) if kv_dtype == "fp8_e4m3fn" else "auto"
+        precision = str(rng.choice(["auto", "fp8", "bf16"])) if kv_dtype == "fp8_e4m3fn" else "auto"
+        if precision == "fp8" and cfg.actual_history_len < 2048:
+            precision = "auto"
         return cfg, kv_dtype, precision
     raise AssertionError("no valid configuration drawn")
 
@@ -89,15 +92,5 @@ def test_random_prefill(i, cuda_device):
           f"mean={lse_diff.mean():.3e}", flush=True)
     mode = "bf16" if prefill.history.uses_bf16_mfma(precision) else "fp8"
     lse_max, lse_mean = LSE_TOL[mode]
-    if mode == "fp8" and cfg.actual_history_len < 2048:
-        # short e4m3 histories: hold the step to the history kernel's own e4m3 error
-        hist = prefill.history(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len,
-                               k_scale=problem.k_scale, v_scale=problem.v_scale, precision=precision)
-        torch.cuda.synchronize()
-        h_max, h_mean = orc.max_abs_and_mean_abs(hist.float().cpu().numpy(),
-                                                 orc.expected_stacked(q, k, v, orc.OracleShape.from_config(cfg)))
-        print(f"  short e4m3 history: history alone max_abs={h_max:.3e} mean_abs={h_mean:.3e}", flush=True)
-        assert max_abs <= max(MAX_ABS_TOL, h_max + 4e-3) and mean_abs <= max(MEAN_ABS_TOL, h_mean + 1e-3)
-        return
     assert max_abs <= MAX_ABS_TOL and mean_abs <= MEAN_ABS_TOL
     assert lse_diff.max() <= lse_max and lse_diff.mean() <= lse_mean
