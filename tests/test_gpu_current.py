@@ -130,6 +130,26 @@ def test_current_causal_only(name, cuda_device):
     assert torch.equal(first, vc[:, 0].repeat_interleave(group, dim=0)), "token 0 output != its V"
 
 
+def test_current_causal_rescales_on_growing_scores(cuda_device):
+    """Current keys scaled up along the sequence (x1 to x7): every row's
+    running max grows by more than the lazy threshold several times, so the
+    head_dim-256 BF16 step rescales O^T in its accumulation registers with
+    non-zero contents; every row against float64."""
+    problem = build_workload_problem("four-chip-fp8", seed=27)
+    cfg = problem.config
+    print(f"case growing scores: current_len={cfg.current_len} D={cfg.head_dim}", flush=True)
+    kc, vc, _, vc64 = _current_kv(cfg, seed=28)
+    ramp = 1.0 + 6.0 * torch.arange(cfg.current_len, dtype=torch.float32) / cfg.current_len
+    kc = (kc.float() * ramp[None, :, None]).to(torch.bfloat16)
+    out, lse = CurrentAttentionKernel(cfg)(problem.q_stacked.to(cuda_device),
+                                           stack_current_kv(kc, vc).to(cuda_device), return_lse=True)
+    torch.cuda.synchronize()
+    shape = orc.OracleShape.from_config(cfg)
+    eo, el = orc.expected_with_current(problem.inputs.q.double().numpy(), kc.double().numpy(), vc64, shape)
+    _assert_close(out.float().cpu().numpy(), eo, "growing scores causal")
+    _assert_lse(lse.cpu().numpy(), el, "bf16", "growing scores causal")
+
+
 @pytest.mark.parametrize(
     "name,precision,exp2",
     [

@@ -322,3 +322,10 @@ def test_dense_fixup_equals_the_bf16_kernel(cuda_device):
     torch.cuda.synchronize()
     assert torch.equal(auto, bf16)
     assert torch.equal(lse, lse16)
+    # and both against float64: scores this peaked raise the running max past
+    # the lazy threshold mid-walk (O^T rescaled in place)
+    sample = _sample(cfg, 96, 46)
+    ref_out, ref_lse = _paged_reference(problem, q.cpu(), sample, problem.page_valid_len, with_lse=True)
+    _check_bar(_pick(bf16, sample), ref_out, "Q x4 bf16")
+    got_lse = np.array([float(lse16[r, h, t]) for r, h, t in sample])
+    assert np.abs(got_lse - ref_lse).max() <= 1e-4
