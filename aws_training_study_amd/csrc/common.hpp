@@ -175,6 +175,15 @@ __device__ __forceinline__ v2i e4m3x4_to_bf16x4(int codes) {
 // s_waitcnt vmcnt(0) with expcnt/lgkmcnt left unconstrained (gfx9 encoding).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// f(std::integral_constant<int, i>{}) for i = I .. N-1, unrolled at compile time.
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
 // Transposing LDS reads as inline asm.  The builtins carry no memory-operand
 // information, so the compiler orders them after every in-flight LDS DMA,
 // including the prefetch of the *other* buffer, which would serialise the

@@ -20,14 +20,6 @@ constexpr float kMaxFloor = -1.0e30f;
 // partial tile that lie past its valid length.
 __device__ __attribute__((aligned(16))) uint8_t zero_chunk[16];
 
-template <int I, int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-    if constexpr (I < N) {
-        f(std::integral_constant<int, I>{});
-        static_for<I + 1, N>(f);
-    }
-}
-
 template <int OFF>
 __device__ __forceinline__ v4i ds_read_b128(uint32_t addr) {
     static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");

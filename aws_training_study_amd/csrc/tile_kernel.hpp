@@ -313,35 +313,39 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
                 for (int e2 = 0; e2 < 8; ++e2) pop[t][u][e2] = (__bf16)s[t][8 * u + e2];
         // A operand lane (d row 16*(grp&1)+gl, k-group grp>>1): for score
         // tile t and half u, keys 32t + 16u + 8*(grp>>1) + [0, 8) of column
-        // d, 4 per transposing read.
+        // d, 4 per transposing read.  Step 2 dt + t takes score tile t of d
+        // tile dt (two MFMAs); its four reads are issued one step ahead, so
+        // that the LDS latency hides behind the previous step's MFMAs.
         // The second buffer of a 32 KB tile lies beyond the 16-bit immediate:
         // its 64 KB part goes into the address.
         constexpr uint32_t VHI = VBASE & ~0xFFFFu;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
+        constexpr int STEPS = 2 * DT;
+        v2i buf[2][4];
+        auto issue = [&](auto sc) {
+            constexpr int step = decltype(sc)::value, dt = step >> 1, t = step & 1;
+            constexpr int o0 = (VBASE + 32 * t * ROW) & 0xFFFF, o1 = (VBASE + (32 * t + 16) * ROW) & 0xFFFF;
             const uint32_t a0 = (L.v_addr[0] ^ ((4 * dt) << 4)) + VHI;
             const uint32_t a1 = (L.v_addr[1] ^ ((4 * dt) << 4)) + VHI;
-            v2i x[4];
-            x[0] = ds_read_tr16_b64<(VBASE) & 0xFFFF>(a0);
-            x[1] = ds_read_tr16_b64<(VBASE) & 0xFFFF>(a1);
-            x[2] = ds_read_tr16_b64<(VBASE + 16 * ROW) & 0xFFFF>(a0);
-            x[3] = ds_read_tr16_b64<(VBASE + 16 * ROW) & 0xFFFF>(a1);
+            v2i(&x)[4] = buf[step & 1];
+            x[0] = ds_read_tr16_b64<o0>(a0);
+            x[1] = ds_read_tr16_b64<o0>(a1);
+            x[2] = ds_read_tr16_b64<o1>(a0);
+            x[3] = ds_read_tr16_b64<o1>(a1);
+        };
+        issue(std::integral_constant<int, 0>{});
+        static_for<0, STEPS>([&](auto sc) {
+            constexpr int step = decltype(sc)::value, dt = step >> 1, t = step & 1;
+            v2i(&x)[4] = buf[step & 1];
             lds_results_ready(x);
+            if constexpr (step + 1 < STEPS) issue(std::integral_constant<int, step + 1>{});
+            __builtin_amdgcn_sched_barrier(0);
             const v4i aop0 = {x[0][0], x[0][1], x[1][0], x[1][1]};
             const v4i aop1 = {x[2][0], x[2][1], x[3][0], x[3][1]};
-            st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop0), pop[0][0], st.o[dt], 0, 0, 0);
-            st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop1), pop[0][1], st.o[dt], 0, 0, 0);
-            v2i y[4];
-            y[0] = ds_read_tr16_b64<(VBASE + 32 * ROW) & 0xFFFF>(a0);
-            y[1] = ds_read_tr16_b64<(VBASE + 32 * ROW) & 0xFFFF>(a1);
-            y[2] = ds_read_tr16_b64<(VBASE + 48 * ROW) & 0xFFFF>(a0);
-            y[3] = ds_read_tr16_b64<(VBASE + 48 * ROW) & 0xFFFF>(a1);
-            lds_results_ready(y);
-            const v4i aop2 = {y[0][0], y[0][1], y[1][0], y[1][1]};
-            const v4i aop3 = {y[2][0], y[2][1], y[3][0], y[3][1]};
-            st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop2), pop[1][0], st.o[dt], 0, 0, 0);
-            st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop3), pop[1][1], st.o[dt], 0, 0, 0);
-        }
+            st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop0), pop[t][0], st.o[dt], 0, 0, 0);
+            st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop1), pop[t][1], st.o[dt], 0, 0, 0);
+            // (the barriers keep the next step's reads ahead of both MFMAs)
+            __builtin_amdgcn_sched_barrier(0);
+        });
     }
 }
 
