@@ -158,21 +158,41 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
 
     // ---- S^T = K . Q^T : two 32-key x 32-query tiles --------------------
     v16f s[2];
+    if constexpr (FP8) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        s[t] = v16f{};
+        for (int t = 0; t < 2; ++t) {
+            s[t] = v16f{};
 #pragma unroll
-        for (int c = 0; c < QK; ++c) {
-            const uint8_t* const kt = lk + t * S::K_T1_ROWS * ROW;
-            if constexpr (FP8) {
+            for (int c = 0; c < QK; ++c) {
+                const uint8_t* const kt = lk + t * S::K_T1_ROWS * ROW;
                 const v4i lo = *(const v4i*)(kt + (L.k_addr ^ ((4 * c) << 4)));
                 const v4i hi = *(const v4i*)(kt + (L.k_addr ^ ((4 * c + 1) << 4)));
                 const v8i aop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 s[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aop, qop[c], s[t], 0, 0, 0, 0, 0, 0);
-            } else {
-                const v4i x = *(const v4i*)(kt + (L.k_addr ^ ((2 * c) << 4)));
-                s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, x), qop[c], s[t], 0, 0, 0);
             }
+        }
+    } else {
+        // both score tiles advance together, their K operands read one
+        // d step ahead of the MFMAs
+        const uint8_t* const kt1 = lk + S::K_T1_ROWS * ROW;
+        v4i kb[2][2];
+        auto load = [&](v4i (&k)[2], int c) {
+            k[0] = *(const v4i*)(lk + (L.k_addr ^ ((2 * c) << 4)));
+            k[1] = *(const v4i*)(kt1 + (L.k_addr ^ ((2 * c) << 4)));
+        };
+        s[0] = v16f{};
+        s[1] = v16f{};
+        load(kb[0], 0);
+#pragma unroll
+        for (int c = 0; c < QK; ++c) {
+            if (c + 1 < QK) load(kb[(c + 1) & 1], c + 1);
+            // (the barriers keep the reads of step c + 1 ahead of step c's MFMAs)
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, kb[c & 1][t]), qop[c], s[t], 0,
+                                                               0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
