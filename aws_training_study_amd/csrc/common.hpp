@@ -162,6 +162,22 @@ __device__ __forceinline__ int chunk_swizzle_v(int row) {
     return chunk_swizzle<FP8, CHUNKS>(row);
 }
 
+// s = -inf unless K < lim, through vcc alone.  Written as plain C++ over a
+// whole score tile, the compiler forms one SGPR-pair mask per element (about
+// 64 SGPRs live at once), which pushes the loop's scalar state into VGPR
+// lanes; this form needs no SGPR beyond vcc.  (-inf comes from a VGPR: vcc
+// and a literal together exceed the one scalar operand a VALU op may read.)
+template <int K>
+__device__ __forceinline__ float mask_key_at_or_past(float s, int lim, float ninf) {
+    static_assert(K >= 0 && K <= 64, "K must be an inline constant");
+    asm("v_cmp_lt_i32_e32 vcc, %1, %2\n\t"
+        "v_cndmask_b32_e32 %0, %3, %0, vcc"
+        : "+v"(s)
+        : "i"(K), "v"(lim), "v"(ninf)
+        : "vcc");
+    return s;
+}
+
 // Four bf16 values (8 bytes) widened exactly from four e4m3 codes (one dword).
 __device__ __forceinline__ v2i e4m3x4_to_bf16x4(int codes) {
     const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(codes, false);

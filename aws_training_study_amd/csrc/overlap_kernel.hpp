@@ -63,11 +63,11 @@ __device__ __forceinline__ void pin(int& x) { asm volatile("" : "+v"(x)); }
 // valid - 32h so that the per-register side is an inline constant.
 __device__ __forceinline__ void mask_tail(v16f (&s)[2], int valid, int h) {
     const int lim = valid - 32 * h;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-            if (16 * t + r >= lim) s[t][r] = -INFINITY;
+    const float ninf = -INFINITY;
+    static_for<0, 32>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        s[k >> 4][k & 15] = mask_key_at_or_past<k>(s[k >> 4][k & 15], lim, ninf);
+    });
 }
 
 }  // namespace ovl
@@ -317,6 +317,18 @@ __device__ __forceinline__ void load_v(const FwdArgs& a, const TileCursor& c, ui
     }
 }
 
+// The four transposing reads of one PV A operand (d tile of `addr`) from V
+// stage VST: keys 32g + 8s + m of the d tile live in LDS rows (8g + m) +
+// {0, 32, 16, 48}[s].
+template <int D, int VST>
+__device__ __forceinline__ void read_v_operand(uint32_t addr, v2i (&x)[4]) {
+    constexpr int off = VST * Shape<D>::TILE, ROW = Shape<D>::ROW;
+    x[0] = ds_read_tr8_b64<off + 0 * ROW>(addr);
+    x[1] = ds_read_tr8_b64<off + 32 * ROW>(addr);
+    x[2] = ds_read_tr8_b64<off + 16 * ROW>(addr);
+    x[3] = ds_read_tr8_b64<off + 48 * ROW>(addr);
+}
+
 // S half: S^T = K Q^T from K stage KST; operand reads one MFMA ahead (the
 // other wave on the SIMD covers the latency).  PREFETCH_V: the last slot
 // starts the first V-operand read of the PV half that follows (stage VST).
@@ -354,12 +366,7 @@ __device__ __forceinline__ void s_half(uint32_t k_addr, uint32_t v_addr, const v
         if constexpr (op + 1 < S::NX) {
             issue_k(std::integral_constant<int, op + 1>{});
         } else if constexpr (PREFETCH_V) {
-            // keys 32g + 8s + m of the d tile live in LDS rows (8g + m) + {0, 32, 16, 48}[s]
-            constexpr int off = VST * S::TILE;
-            xv[0] = ds_read_tr8_b64<off + 0 * S::ROW>(v_addr);
-            xv[1] = ds_read_tr8_b64<off + 32 * S::ROW>(v_addr);
-            xv[2] = ds_read_tr8_b64<off + 16 * S::ROW>(v_addr);
-            xv[3] = ds_read_tr8_b64<off + 48 * S::ROW>(v_addr);
+            read_v_operand<D, VST>(v_addr, xv);
         }
         const v4i lo = kr[op & 1][0], hi = kr[op & 1][1];
         const v8i kop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -389,13 +396,7 @@ __device__ __forceinline__ void pv_half(uint32_t v_addr, v2i (&xv0)[4], v16f (&o
     };
     auto issue_v = [&](auto dc) {
         constexpr int dt = decltype(dc)::value;
-        constexpr int off = VST * S::TILE;
-        const uint32_t addr = v_addr ^ ((2 * dt) << 4);
-        v2i(&x)[4] = buf(dc);
-        x[0] = ds_read_tr8_b64<off + 0 * S::ROW>(addr);
-        x[1] = ds_read_tr8_b64<off + 32 * S::ROW>(addr);
-        x[2] = ds_read_tr8_b64<off + 16 * S::ROW>(addr);
-        x[3] = ds_read_tr8_b64<off + 48 * S::ROW>(addr);
+        read_v_operand<D, VST>(v_addr ^ ((2 * dt) << 4), buf(dc));
     };
     if constexpr (!PREFETCHED) issue_v(std::integral_constant<int, 0>{});
     static_for<0, S::DT>([&](auto dc) {
@@ -421,7 +422,8 @@ __device__ __forceinline__ void pv_half(uint32_t v_addr, v2i (&xv0)[4], v16f (&o
 template <int D, int J4, bool LATE, bool FAST, int DMAW>
 __device__ __forceinline__ void iteration(const FwdArgs& a, uint8_t* lds, int wave, int h, const Lanes& L,
                                           const v8i (&q)[Shape<D>::QK], v16f (&s)[2], v8i (&pbuf)[2],
-                                          v16f (&o)[Shape<D>::DT], SoftmaxRow& sm, Cursors& cs, int head) {
+                                          v16f (&o)[Shape<D>::DT], SoftmaxRow& sm, Cursors& cs, int head,
+                                          v2i (&xv)[4]) {
     using S = Shape<D>;
     constexpr int KST = J4;  // K(j)
 
@@ -450,7 +452,6 @@ __device__ __forceinline__ void iteration(const FwdArgs& a, uint8_t* lds, int wa
         load_v<S, P>(a, cs.c1, lds, (J4 + 1) % kStages, wave_off, L.dma_v, is_real(a, cs.c1));
     }
 
-    v2i xv[4];
     if constexpr (!LATE) {
         // S(j), then PV(j-1) beside softmax(j)
         constexpr int VST = (J4 + 3) % kStages;
@@ -458,11 +459,14 @@ __device__ __forceinline__ void iteration(const FwdArgs& a, uint8_t* lds, int wa
         pv_half<D, VST, true, FAST>(v_addr, xv, o, pbuf[(J4 + 1) & 1], s, pbuf[J4 & 1], sm,
                               cs.k0, h);
     } else {
-        // PV(j-2) beside softmax(j-1), then S(j)
+        // PV(j-2) beside softmax(j-1), then S(j).  The first V-operand read
+        // of PV(j-2) was issued at the end of the previous iteration's S half
+        // (V(j-2) landed before the previous barrier), so it is in flight
+        // across the barrier; this S half issues the one for PV(j-1).
         constexpr int VST = (J4 + 2) % kStages;
-        pv_half<D, VST, false, FAST>(v_addr, xv, o, pbuf[J4 & 1], s, pbuf[(J4 + 1) & 1], sm,
-                               cs.km1, h);
-        s_half<D, KST, false, 0>(k_addr, v_addr, q, s, xv, pbuf[J4 & 1], sm, L.rsel);
+        pv_half<D, VST, true, FAST>(v_addr, xv, o, pbuf[J4 & 1], s, pbuf[(J4 + 1) & 1], sm,
+                              cs.km1, h);
+        s_half<D, KST, true, (J4 + 3) % kStages>(k_addr, v_addr, q, s, xv, pbuf[J4 & 1], sm, L.rsel);
     }
 
     cs.km1 = cs.k0;
@@ -476,21 +480,28 @@ template <int D, bool LATE, bool FAST, int DMAW>
 __device__ __forceinline__ void walk(const FwdArgs& a, uint8_t* lds, int wave, int h, const Lanes& L,
                                      const v8i (&q)[Shape<D>::QK], v16f (&s)[2], v8i (&pbuf)[2],
                                      v16f (&o)[Shape<D>::DT], SoftmaxRow& sm, Cursors cs, int head) {
+    // the first V-operand read of the next PV half (the PV-first waves start
+    // with PV(-2): V stage 2, zeros)
+    v2i xv[4];
+    if constexpr (LATE) read_v_operand<D, 2>(L.v_addr, xv);
     for (;;) {
         // after iteration j the loop ends if tile j-1 was past the last tile
         bool done = cs.km1 < 0;
-        iteration<D, 0, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+        iteration<D, 0, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head, xv);
         if (done) break;
         done = cs.km1 < 0;
-        iteration<D, 1, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+        iteration<D, 1, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head, xv);
         if (done) break;
         done = cs.km1 < 0;
-        iteration<D, 2, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+        iteration<D, 2, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head, xv);
         if (done) break;
         done = cs.km1 < 0;
-        iteration<D, 3, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
+        iteration<D, 3, LATE, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head, xv);
         if (done) break;
     }
+    // the PV-first waves' last S half read an operand of a PV half that does
+    // not run: let it land before its registers are reused
+    if constexpr (LATE) lds_wait<0>(xv);
 }
 
 // Byte offset of query row `row` of KV head `head` (rows past the last are
@@ -515,7 +526,7 @@ template <int D, bool FAST, bool LSE, bool SPLIT = false>
 __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     using S = Shape<D>;
     constexpr int QK = S::QK, DT = S::DT, ROW = S::ROW, CHUNKS = S::CHUNKS;
-    constexpr int DMAW = SPLIT ? kWaves : kWaves / 2;
+    constexpr int DMAW = kWaves / 2;
     using P = DmaPlan<D, DMAW>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * S::RING];
 

@@ -199,11 +199,15 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
     // ---- mask, online softmax (lazy rescale) ----------------------------
     // (CAUSAL: only tiles that cross some row's limit, a wave-uniform test)
     if (CAUSAL ? __builtin_amdgcn_ballot_w64(valid < kKeyTile) != 0 : valid < kKeyTile) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                if (key_of_acc<FP8>(t, r, h) >= valid) s[t][r] = -INFINITY;
+        // key_of_acc(t, r, h) >= valid, as its lane-independent part against
+        // valid less its lane-half part
+        const int lim = valid - key_of_acc<FP8>(0, 0, h);
+        const float ninf = -INFINITY;
+        static_for<0, 32>([&](auto kc) {
+            constexpr int t = decltype(kc)::value >> 4, r = decltype(kc)::value & 15;
+            constexpr int k = FP8 ? 16 * t + r : 32 * t + 16 * (r >> 3) + (r & 7);
+            s[t][r] = mask_key_at_or_past<k>(s[t][r], lim, ninf);
+        });
     }
     float mx = -INFINITY;
 #pragma unroll
