@@ -92,7 +92,9 @@ __device__ __forceinline__ void mask_tail(v16f (&s)[2], int valid, int h) {
 // the matrix core alone while the other interleaves its PV MFMAs with its
 // softmax.  One barrier per iteration.  K and V tiles live in separate
 // four-stage LDS rings (tile t in stage t % 4): K(j+2) and V(j+1) are
-// requested at the top of iteration j.  Tiles before the first and after
+// requested in iteration j, one 1 KB block per PV MFMA of the PV-first group
+// (the LDS-DMA writes then reach the LDS spread over the iteration rather
+// than in one burst that stalls every wave's operand reads).  Tiles before the first and after
 // the last are "phantom" tiles without valid keys: their scores are masked
 // to -inf (P = 0, softmax state unchanged, since the running max starts at
 // a finite floor) and their V stages hold zeros (zeroed up front for tiles
@@ -125,16 +127,14 @@ struct Shape {
     }
 };
 
-// Who moves the K and V tiles: the last WAVES waves of the workgroup issue
-// the LDS-DMA of every K and V tile and each waits for its own blocks; the
-// barrier after the waits publishes them to all waves.  WAVES = kWaves / 2
-// is the group that runs PV first (one wave per SIMD); with it the plain and
-// log-sum-exp launches measured about 1% faster than with all eight waves
-// issuing.  The split instantiations spill Q fragments inside the loop with
-// four issuing waves, so they keep WAVES = kWaves.
+// Who moves the K and V tiles: the last WAVES = kWaves / 2 waves of the
+// workgroup, the group that runs PV first (one wave per SIMD), issue the
+// LDS-DMA of every K and V tile and each waits for its own blocks; the
+// barrier after the waits publishes them to all waves (about 1% faster than
+// all eight waves issuing).
 template <int D, int WAVES>
 struct DmaPlan {
-    static_assert(WAVES == kWaves || WAVES == kWaves / 2, "DMA from all waves or from the late group");
+    static_assert(WAVES == kWaves / 2, "the PV-first group issues all DMA");
     static constexpr int ROW = D;
     static constexpr int DPW = kKeyTile * ROW / 1024 / WAVES;  // 1 KB blocks per wave per K (or V) tile
     static constexpr int STRIDE = WAVES * 1024;                // LDS bytes between a wave's blocks
@@ -156,7 +156,7 @@ struct DmaPlan {
 struct Lanes {
     uint32_t k_addr;  // score operand, K stage 0, k-step 0, low 16 bytes
     uint32_t v_addr;  // PV operand, V stage 0, d tile 0 (includes the ring offset)
-    uint32_t dma_k;   // byte offset of the lane's K chunk of DMA block `wave` in a tile
+    uint32_t dma_k;   // byte offset of the lane's K chunk of its DMA block 0 in a tile, plus DmaPlan::MID
     uint32_t dma_v;   // same for V (its own swizzle)
     int rsel;         // row-sum selector operand word (see s_half)
 };
@@ -267,54 +267,92 @@ __device__ __forceinline__ int dma_chunk_key(int i, int wave_off) {
     return lds_row<true>((i * P::STRIDE + wave_off + __lane_id() * 16) / P::ROW);
 }
 
-// DMA blocks I.. of a full tile into dst.  mid is the lane's source address
-// of block 0 plus P::MID: the blocks' offsets from it are immediates of the
-// loads rather than 64-bit constants held in registers.  The immediate is
-// added to the LDS address as well, so the LDS operand is taken that much
-// lower (it stays non-negative: imm <= MID < STRIDE <= I * STRIDE for I > 0).
+// LDS-DMA of one 1 KB block: lane l copies 16 bytes from global memory into
+// LDS byte m0v + IMM + 16 l (the instruction offset IMM applies to both
+// addresses).  Inline asm rather than the builtin, for the scalar-base form:
+// the wave-uniform tile address stays in an SGPR pair and each lane adds one
+// 32-bit VGPR offset, where the builtin forms a 64-bit VGPR address per lane
+// (registers the S half does not have).  Every LDS-DMA of this kernel goes
+// through these two helpers, so m0 never holds a value of the compiler's own
+// across them; s_nop 0 covers the m0 write ahead of the load.
+template <int IMM>
+__device__ __forceinline__ void dma_sbase(const uint8_t* base, uint32_t lane_off, uint32_t m0v) {
+    static_assert(IMM >= -4096 && IMM < 4096, "the instruction offset is 13-bit signed");
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:%3"
+                 :
+                 : "s"(m0v), "v"(lane_off), "s"(base), "i"(IMM)
+                 : "memory", "m0");
+}
+// The same from a per-lane 64-bit address, without an offset.
+__device__ __forceinline__ void dma_vaddr(const uint8_t* addr, uint32_t m0v) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(m0v), "v"(addr)
+                 : "memory", "m0");
+}
+
+// DMA block I of a full tile at `tile` into LDS at `dst` (the LDS address of
+// the wave's block 0 in the stage).  lane_mid is the lane's chunk offset in
+// the tile plus P::MID: the blocks' offsets from it are the loads'
+// immediates, and m0 is taken that much lower (it stays inside the block:
+// imm <= MID < STRIDE <= I * STRIDE for I > 0).
+template <class P, int I>
+__device__ __forceinline__ void dma_block(const uint8_t* tile, uint32_t lane_mid, uint32_t dst) {
+    constexpr int imm = P::offset(I) - P::MID;
+    static_assert(I == 0 || imm < I * P::STRIDE, "m0 must stay inside the block");
+    dma_sbase<imm>(tile, lane_mid, dst + (I * P::STRIDE - imm));
+}
 template <class P, int I = 0>
-__device__ __forceinline__ void dma_blocks(const uint8_t* mid, uint8_t* dst) {
+__device__ __forceinline__ void dma_blocks(const uint8_t* tile, uint32_t lane_mid, uint32_t dst) {
     if constexpr (I < P::DPW) {
-        constexpr int imm = P::offset(I) - P::MID;
-        static_assert(I == 0 || imm < I * P::STRIDE, "LDS operand must stay inside the block");
-        uint8_t* const d = dst + (I * P::STRIDE - imm);
-        __builtin_amdgcn_global_load_lds(mid, PCPA_LDS(void, d), 16, imm, 0);
-        dma_blocks<P, I + 1>(mid, dst);
+        dma_block<P, I>(tile, lane_mid, dst);
+        dma_blocks<P, I + 1>(tile, lane_mid, dst);
     }
 }
 
-// Issue the K tile of cursor c into K stage st.  (Pointers are formed in
-// plain variables: address-space casts of expressions that depend on S trip
-// the host compilation pass.)
-template <class S, class P>
-__device__ __forceinline__ void load_k(const FwdArgs& a, const TileCursor& c, uint8_t* lds, int st, int wave_off,
-                                       uint32_t off) {
-    const uint8_t* const kt = a.kv + c.k_off + (int64_t)c.base * S::ROW + off + P::MID;
-    dma_blocks<P>(kt, lds + st * S::TILE + wave_off);
+// Global addresses of cursor c's K and V tiles (wave-uniform).
+template <class S>
+__device__ __forceinline__ const uint8_t* k_tile(const FwdArgs& a, const TileCursor& c) {
+    return a.kv + c.k_off + (int64_t)c.base * S::ROW;
+}
+template <class S>
+__device__ __forceinline__ const uint8_t* v_tile(const FwdArgs& a, const TileCursor& c) {
+    return k_tile<S>(a, c) + (int64_t)a.num_kv_heads * a.head_stride;
 }
 
-// Issue the V tile of cursor c into V stage st.  Rows past the valid length
-// (all rows of a phantom tile) come from zero_chunk, so V stages of masked
-// keys hold zeros and the number of loads per tile never changes.
+// Issue the K tile of cursor c into K stage st (lds: LDS address of the
+// rings).  A phantom tile's cursor reads the pool's first tile (k_off 0),
+// so that every iteration issues the same loads.
 template <class S, class P>
-__device__ __forceinline__ void load_v(const FwdArgs& a, const TileCursor& c, uint8_t* lds, int st, int wave_off,
-                                       uint32_t off, bool real) {
-    const uint8_t* const vt =
-        a.kv + c.k_off + (int64_t)c.base * S::ROW + (int64_t)a.num_kv_heads * a.head_stride + off + P::MID;
-    uint8_t* const dst = lds + S::RING + st * S::TILE + wave_off;
-    const int valid = real ? c.n - c.base : 0;
-    if (valid >= kKeyTile) {
-        dma_blocks<P>(vt, dst);
-    } else {
-        const uint8_t* const zero = zero_chunk;
+__device__ __forceinline__ void load_k(const FwdArgs& a, const TileCursor& c, uint32_t lds, int st, int wave_off,
+                                       uint32_t lane_mid) {
+    dma_blocks<P>(k_tile<S>(a, c), lane_mid, lds + st * S::TILE + wave_off);
+}
+
+// The V tile of cursor c with `valid` (< 64) valid keys into V stage st:
+// rows past the valid length (all rows of a phantom tile) come from
+// zero_chunk, so V stages of masked keys hold zeros.
+template <class S, class P>
+__device__ __forceinline__ void load_v_partial(const FwdArgs& a, const TileCursor& c, uint32_t lds, int st,
+                                               int wave_off, uint32_t lane_mid, int valid) {
+    const uint8_t* const vt = v_tile<S>(a, c) + lane_mid;
+    const uint32_t dst = lds + S::RING + st * S::TILE + wave_off;
 #pragma unroll
-        for (int i = 0; i < P::DPW; ++i) {
-            const uint8_t* const src =
-                dma_chunk_key<P>(i, wave_off) < valid ? vt + (P::offset(i) - P::MID) : zero;
-            uint8_t* const d = dst + i * P::STRIDE;
-            __builtin_amdgcn_global_load_lds(src, PCPA_LDS(void, d), 16, 0, 0);
-        }
+    for (int i = 0; i < P::DPW; ++i) {
+        const uint8_t* const src = dma_chunk_key<P>(i, wave_off) < valid ? vt + (P::offset(i) - P::MID) : zero_chunk;
+        dma_vaddr(src, dst + i * P::STRIDE);
     }
+}
+
+// Issue the V tile of cursor c into V stage st (real: c is a tile).
+template <class S, class P>
+__device__ __forceinline__ void load_v(const FwdArgs& a, const TileCursor& c, uint32_t lds, int st, int wave_off,
+                                       uint32_t lane_mid, bool real) {
+    const int valid = real ? c.n - c.base : 0;
+    if (valid >= kKeyTile)
+        dma_blocks<P>(v_tile<S>(a, c), lane_mid, lds + S::RING + st * S::TILE + wave_off);
+    else
+        load_v_partial<S, P>(a, c, lds, st, wave_off, lane_mid, valid);
 }
 
 // The four transposing reads of one PV A operand (d tile of `addr`) from V
@@ -371,20 +409,28 @@ __device__ __forceinline__ void s_half(uint32_t k_addr, uint32_t v_addr, const v
         const v4i lo = kr[op & 1][0], hi = kr[op & 1][1];
         const v8i kop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         s[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kop, q[c], c == 0 ? v16f{} : s[t], 0, 0, 0, 0, 0, 0);
+        if constexpr (op == 1) {
+            // The row sum has long completed (two score MFMAs since): read
+            // it, then free its registers.  All 4 stay allocated until the
+            // read: the inline-asm LDS reads are invisible to the hazard
+            // checks and must not be given registers that the in-flight
+            // MFMA is still going to write.  (The read waits for the MFMA;
+            // the tie after it keeps the later reads behind it.)
+            sm.l = fmaf(rowsum[0], sm.alpha, sm.l);
+            asm volatile("" : "+v"(rowsum));
+        }
     });
-    // All 4 row-sum registers stay allocated until here: the inline-asm LDS
-    // reads above are invisible to the hazard checks and must not be given
-    // registers that the in-flight MFMA is still going to write.
-    asm volatile("" : "+v"(rowsum));
-    sm.l = fmaf(rowsum[0], sm.alpha, sm.l);
 }
 
 // PV half: O^T += V^T P_old^T from V stage VST, beside the softmax of s
 // (valid keys < valid) into p_new; then the lazy O^T rescale.  PREFETCHED:
-// the first V-operand read was issued by the S half.
-template <int D, int VST, bool PREFETCHED, bool FAST>
+// the first V-operand read was issued by the S half.  after_mfma(dt) runs
+// after PV MFMA dt is issued (the DMA-issuing waves spread their tile
+// loads over the PV half there, one block per MFMA).
+template <int D, int VST, bool PREFETCHED, bool FAST, class Hook>
 __device__ __forceinline__ void pv_half(uint32_t v_addr, v2i (&xv0)[4], v16f (&o)[Shape<D>::DT], const v8i& p_old,
-                                        v16f (&s)[2], v8i& p_new, SoftmaxRow& sm, int valid, int h) {
+                                        v16f (&s)[2], v8i& p_new, SoftmaxRow& sm, int valid, int h,
+                                        Hook&& after_mfma) {
     using S = Shape<D>;
     if (valid < kKeyTile) mask_tail(s, valid, h);
     v2i xv1[4];
@@ -406,6 +452,7 @@ __device__ __forceinline__ void pv_half(uint32_t v_addr, v2i (&xv0)[4], v16f (&o
         if constexpr (dt + 1 < S::DT) issue_v(std::integral_constant<int, dt + 1>{});
         const v8i vop = {x[0][0], x[0][1], x[1][0], x[1][1], x[2][0], x[2][1], x[3][0], x[3][1]};
         o[dt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vop, p_old, o[dt], 0, 0, 0, 0, 0, 0);
+        after_mfma(dc);
         softmax_slices<S::pv_begin(dt), S::pv_begin(dt + 1), FAST>(s, p_new, sm);
         __builtin_amdgcn_sched_barrier(0);
     });
@@ -428,44 +475,53 @@ __device__ __forceinline__ void iteration(const FwdArgs& a, uint8_t* lds, int wa
     constexpr int KST = J4;  // K(j)
 
     // ---- K(j) and V(j-1) have landed (for every wave) ----------------------
-    // Loads issued one iteration ago may be pending: V(j), and K(j+1) if tile
-    // j+1 is real.  Each wave that issues DMA waits for its own blocks; the
+    // Loads issued one iteration ago may be pending: V(j) and K(j+1) (a
+    // phantom K tile is loaded too).  Each wave that issues DMA waits for its own blocks; the
     // barrier then publishes all of them.
     using P = DmaPlan<D, DMAW>;
-    constexpr bool dma = DMAW == kWaves || LATE;
-    if constexpr (dma) {
-        if (is_real(a, cs.c1))
-            wait_vmem_le<2 * P::DPW>();
-        else
-            wait_vmem_le<P::DPW>();
-    }
+    if constexpr (LATE) wait_vmem_le<2 * P::DPW>();
     __builtin_amdgcn_s_barrier();
-    // K stage (j+2) % 4 held K(j-2) and V stage (j+1) % 4 held V(j-3); both
-    // were last read in iteration j-1.  The wave offset and operand bases
+    // The wave offset and operand bases
     // are made opaque so that the DMA destinations and operand addresses are
     // recomputed in the loop rather than hoisted and spilled.
     int wave_off = P::block(wave) * 1024;
     uint32_t k_addr = L.k_addr, v_addr = L.v_addr;
     asm volatile("" : "+s"(wave_off), "+v"(k_addr), "+v"(v_addr));
-    if constexpr (dma) {
-        if (is_real(a, cs.c2)) load_k<S, P>(a, cs.c2, lds, (J4 + 2) % kStages, wave_off, L.dma_k);
-        load_v<S, P>(a, cs.c1, lds, (J4 + 1) % kStages, wave_off, L.dma_v, is_real(a, cs.c1));
-    }
-
     if constexpr (!LATE) {
         // S(j), then PV(j-1) beside softmax(j)
         constexpr int VST = (J4 + 3) % kStages;
         s_half<D, KST, true, VST>(k_addr, v_addr, q, s, xv, pbuf[J4 & 1], sm, L.rsel);
         pv_half<D, VST, true, FAST>(v_addr, xv, o, pbuf[(J4 + 1) & 1], s, pbuf[J4 & 1], sm,
-                              cs.k0, h);
+                              cs.k0, h, [](auto) {});
     } else {
         // PV(j-2) beside softmax(j-1), then S(j).  The first V-operand read
         // of PV(j-2) was issued at the end of the previous iteration's S half
         // (V(j-2) landed before the previous barrier), so it is in flight
         // across the barrier; this S half issues the one for PV(j-1).
         constexpr int VST = (J4 + 2) % kStages;
+        // This group's DMA of K(j+2) and V(j+1) is spread over its PV half,
+        // one block per PV MFMA: K after the first DPW, V after the next DPW
+        // (a V tile with masked rows, rare, is issued before the half).  K
+        // stage (j+2) % 4 and V stage (j+1) % 4 were last read in iteration
+        // j-1, before this iteration's barrier.
+        const uint32_t lds_u = lds_address(lds);
+        const bool v_real = is_real(a, cs.c1);
+        const int v_valid = v_real ? cs.c1.n - cs.c1.base : 0;
+        if (v_valid < kKeyTile) load_v_partial<S, P>(a, cs.c1, lds_u, (J4 + 1) % kStages, wave_off, L.dma_v, v_valid);
+        const uint8_t* const ktile = k_tile<S>(a, cs.c2);
+        const uint32_t kdst = lds_u + ((J4 + 2) % kStages) * S::TILE + wave_off;
+        const uint8_t* const vtile = v_tile<S>(a, cs.c1);
+        const uint32_t vdst = lds_u + S::RING + ((J4 + 1) % kStages) * S::TILE + wave_off;
+        auto dma_step = [&](auto dc) {
+            constexpr int i = decltype(dc)::value;
+            if constexpr (i < P::DPW) {
+                dma_block<P, i>(ktile, L.dma_k, kdst);
+            } else if constexpr (i < 2 * P::DPW) {
+                if (v_valid >= kKeyTile) dma_block<P, i - P::DPW>(vtile, L.dma_v, vdst);
+            }
+        };
         pv_half<D, VST, true, FAST>(v_addr, xv, o, pbuf[J4 & 1], s, pbuf[(J4 + 1) & 1], sm,
-                              cs.km1, h);
+                              cs.km1, h, dma_step);
         s_half<D, KST, true, (J4 + 3) % kStages>(k_addr, v_addr, q, s, xv, pbuf[J4 & 1], sm, L.rsel);
     }
 
@@ -618,8 +674,8 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
         const int drow = byte / ROW;
         const int pos = (byte % ROW) / 16;
         const int key = lds_row<true>(drow);
-        L.dma_k = key * ROW + (pos ^ chunk_swizzle<true, CHUNKS>(drow)) * 16;
-        L.dma_v = key * ROW + (pos ^ chunk_swizzle_v<true, CHUNKS>(drow)) * 16;
+        L.dma_k = key * ROW + (pos ^ chunk_swizzle<true, CHUNKS>(drow)) * 16 + P::MID;
+        L.dma_v = key * ROW + (pos ^ chunk_swizzle_v<true, CHUNKS>(drow)) * 16 + P::MID;
         L.rsel = ((lane ^ (lane >> 2)) & 4) ? 0 : 0x38383838;
     }
 
@@ -642,12 +698,13 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
         cs.k0 = tile_keys(a, first);
         cs.c1 = next_tile(a, head, first);
         cs.c2 = is_real(a, cs.c1) ? next_tile(a, head, cs.c1) : cs.c1;
-        // K(0), then V(0) and K(1) as if requested at the top of iteration -1.
+        // K(0), then V(0) and K(1) as if requested in iteration -1.
         if (P::issues(wave)) {
             const int wave_off = P::block(wave) * 1024;
-            load_k<S, P>(a, first, lds, 0, wave_off, L.dma_k);
-            load_v<S, P>(a, first, lds, 0, wave_off, L.dma_v, true);
-            if (is_real(a, cs.c1)) load_k<S, P>(a, cs.c1, lds, 1, wave_off, L.dma_k);
+            const uint32_t lds_u = lds_address(lds);
+            load_k<S, P>(a, first, lds_u, 0, wave_off, L.dma_k);
+            load_v<S, P>(a, first, lds_u, 0, wave_off, L.dma_v, true);
+            load_k<S, P>(a, cs.c1, lds_u, 1, wave_off, L.dma_k);
         }
         if (wave < kWaves / 2)
             walk<D, false, FAST, DMAW>(a, lds, wave, h, L, q, s, pbuf, o, sm, cs, head);
@@ -656,21 +713,16 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     }
 
     // ---- epilogue: O = O^T / l, bf16; log-sum-exp ---------------------------
-    // The row, its offset and the lane half again, from an opaque lane id and
-    // opaque divisors: values kept live through the walk (the row offset, the
-    // reciprocals of the row maps' divisors, lane-derived store offsets) take
-    // registers there and spill (outside the loop).  The split
-    // instantiations keep the row and its offset from the prologue instead:
-    // at their register pressure every recomputation tried moved a Q
-    // fragment's spill into the loop.
+    // The row and its offset again, from an opaque lane id and opaque
+    // divisors: values kept live through the walk (the row offset, the
+    // reciprocals of the row maps' divisors) take registers there and spill.
     int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
     asm volatile("" : "+v"(lane_e));
-    const int he = SPLIT ? h : lane_e >> 5;
     FwdArgs ag = a;
     asm volatile("" : "+s"(ag.group_rows), "+s"(ag.local_q));
-    const int row = SPLIT ? q_row : row_tile * kRowsPerGroup + wave * 32 + (lane_e & 31);
+    const int row = row_tile * kRowsPerGroup + wave * 32 + (lane_e & 31);
     const bool row_ok = row < a.rows_per_head;
-    const int64_t row_off = SPLIT ? q_off : query_row_offset<D>(ag, row, head);
+    const int64_t row_off = query_row_offset<D>(ag, row, head);
     const float scale = sm.l > 0.f ? a.v_scale / sm.l : 0.f;
     // sum_k exp(score_k) = l * 2^(m - 6), less the average overestimate of
     // the linear-mantissa exp2

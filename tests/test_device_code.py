@@ -1,10 +1,9 @@
 """Properties of the compiled gfx950 device code (CPU only: hipcc cross-compiles).
 
-* No attention kernel spills to scratch, except the split-history
-  instantiations of the e4m3 head_dim-256 kernel, whose few spills (the row
-  and its offset, kept from the prologue for the epilogue) must stay outside
-  every loop: a Q fragment reloaded from scratch inside the walk cost 30% on
-  the MI355X (8.87 against 6.8 ms on the full 64-rank workload).
+* No attention kernel spills to scratch: a Q fragment reloaded from scratch
+  inside the walk cost 30% on the MI355X (8.87 against 6.8 ms on the full
+  64-rank workload; the reload's vmcnt wait also waits for every LDS-DMA in
+  flight).
 * No LDS read writes a register that an MFMA issued before it is still
   going to write.  The transposing V reads and the score-operand reads are
   inline asm, invisible to the compiler's hazard checks; the kernels keep
@@ -77,21 +76,12 @@ def _scratch_ops(lines):
 
 def test_attention_kernels_do_not_spill(device_code):
     usage, _ = device_code
+    split = [n for n in _attention_kernels(usage) if _is_split_overlap(n)]
+    assert len(split) == 2, split  # the split instantiations (fast and exact exp2) are covered too
     for name in _attention_kernels(usage):
-        if _is_split_overlap(name):
-            continue
         assert usage[name].get("ScratchSize", -1) == 0, (name, usage[name])
         assert usage[name].get("VGPRs Spill", -1) == 0, (name, usage[name])
-
-
-def test_split_overlap_spills_stay_outside_loops(device_code):
-    usage, bodies = device_code
-    split = [n for n in _attention_kernels(usage) if _is_split_overlap(n)]
-    assert len(split) == 2, split  # fast and exact exp2
-    for name in split:
-        assert usage[name]["ScratchSize"] <= 16, (name, usage[name])
-        total, looped = _scratch_ops(bodies[name])
-        assert looped == 0, f"{name}: {looped} of {total} scratch accesses inside a loop"
+        assert usage[name].get("SGPRs Spill", -1) == 0, (name, usage[name])
 
 
 def test_no_scratch_access_inside_any_loop(device_code):
