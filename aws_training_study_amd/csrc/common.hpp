@@ -178,6 +178,31 @@ __device__ __forceinline__ float mask_key_at_or_past(float s, int lim, float nin
     return s;
 }
 
+// LDS-DMA of one 1 KB block: lane l copies 16 bytes from global memory into
+// LDS byte m0v + IMM + 16 l (the instruction offset IMM applies to both
+// addresses).  Inline asm rather than the builtin, for the scalar-base form:
+// the wave-uniform tile address stays in an SGPR pair and each lane adds one
+// 32-bit VGPR offset, where the builtin forms a 64-bit VGPR address per lane
+// (registers the kernels' tile loops do not have).  Every LDS-DMA of the
+// attention kernels goes through these two helpers, so m0 never holds a
+// value of the compiler's own across them; s_nop 0 covers the m0 write
+// ahead of the load.
+template <int IMM>
+__device__ __forceinline__ void dma_sbase(const uint8_t* base, uint32_t lane_off, uint32_t m0v) {
+    static_assert(IMM >= -4096 && IMM < 4096, "the instruction offset is 13-bit signed");
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:%3"
+                 :
+                 : "s"(m0v), "v"(lane_off), "s"(base), "i"(IMM)
+                 : "memory", "m0");
+}
+// The same from a per-lane 64-bit address, without an offset.
+__device__ __forceinline__ void dma_vaddr(const uint8_t* addr, uint32_t m0v) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(m0v), "v"(addr)
+                 : "memory", "m0");
+}
+
 // Four bf16 values (8 bytes) widened exactly from four e4m3 codes (one dword).
 __device__ __forceinline__ v2i e4m3x4_to_bf16x4(int codes) {
     const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(codes, false);
@@ -231,6 +256,9 @@ __device__ __forceinline__ void lds_results_ready(v2i (&x)[8]) {
 }
 __device__ __forceinline__ void lds_results_ready(v2i (&x)[4]) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]));
+}
+__device__ __forceinline__ void lds_results_ready(v2i (&x)[2]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x[0]), "+v"(x[1]));
 }
 
 // Position in the walk over the block table: entry e (rank-major (rank,

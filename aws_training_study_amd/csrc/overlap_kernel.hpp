@@ -267,30 +267,6 @@ __device__ __forceinline__ int dma_chunk_key(int i, int wave_off) {
     return lds_row<true>((i * P::STRIDE + wave_off + __lane_id() * 16) / P::ROW);
 }
 
-// LDS-DMA of one 1 KB block: lane l copies 16 bytes from global memory into
-// LDS byte m0v + IMM + 16 l (the instruction offset IMM applies to both
-// addresses).  Inline asm rather than the builtin, for the scalar-base form:
-// the wave-uniform tile address stays in an SGPR pair and each lane adds one
-// 32-bit VGPR offset, where the builtin forms a 64-bit VGPR address per lane
-// (registers the S half does not have).  Every LDS-DMA of this kernel goes
-// through these two helpers, so m0 never holds a value of the compiler's own
-// across them; s_nop 0 covers the m0 write ahead of the load.
-template <int IMM>
-__device__ __forceinline__ void dma_sbase(const uint8_t* base, uint32_t lane_off, uint32_t m0v) {
-    static_assert(IMM >= -4096 && IMM < 4096, "the instruction offset is 13-bit signed");
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:%3"
-                 :
-                 : "s"(m0v), "v"(lane_off), "s"(base), "i"(IMM)
-                 : "memory", "m0");
-}
-// The same from a per-lane 64-bit address, without an offset.
-__device__ __forceinline__ void dma_vaddr(const uint8_t* addr, uint32_t m0v) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :
-                 : "s"(m0v), "v"(addr)
-                 : "memory", "m0");
-}
-
 // DMA block I of a full tile at `tile` into LDS at `dst` (the LDS address of
 // the wave's block 0 in the stage).  lane_mid is the lane's chunk offset in
 // the tile plus P::MID: the blocks' offsets from it are the loads'

@@ -209,8 +209,8 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
     if (!fn) return PCPA_ERR_UNSUPPORTED;
     void* args[] = {&a};
     const int items = a.row_tiles * p->num_kv_heads * splits;
-    if (hipLaunchKernel(fn, dim3(8 * ((items + 7) / 8)), dim3(overlap ? ovl::kThreads : kThreads), args, 0, stream) !=
-        hipSuccess)
+    const int threads = overlap ? ovl::kThreads : tile_threads(p->head_dim, fp8);
+    if (hipLaunchKernel(fn, dim3(8 * ((items + 7) / 8)), dim3(threads), args, 0, stream) != hipSuccess)
         return PCPA_ERR_LAUNCH;
     if (splits > 1) {
         const int64_t rows = (int64_t)p->pcp_size * p->num_q_heads * p->local_q_len;
@@ -255,7 +255,8 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
             case 256: fix = (const void*)history_fwd_kernel<256, true, false, false, false, true>; break;
             default: return PCPA_ERR_UNSUPPORTED;
         }
-        if (hipLaunchKernel(fix, dim3(grid), dim3(kThreads), bargs, 0, stream) != hipSuccess) return PCPA_ERR_LAUNCH;
+        if (hipLaunchKernel(fix, dim3(grid), dim3(tile_threads(p->head_dim, false)), bargs, 0, stream) != hipSuccess)
+            return PCPA_ERR_LAUNCH;
         const int d_vec8 = p->head_dim / 8;
         const int64_t slot_rows = (int64_t)w.guard_slots * kRowsPerGroup;
         hipLaunchKernelGGL(guard_merge_kernel, dim3((unsigned)slot_rows), dim3(kGuardMergeThreads), 0, stream,
@@ -426,7 +427,8 @@ int32_t pcpa_current_attention(const pcpa_params* p, int32_t interleave, const v
     }
     const int items = a.row_tiles * p->num_kv_heads;
     const hipError_t err =
-        hipLaunchKernel(fn, dim3(8 * ((items + 7) / 8)), dim3(pcpa::kThreads), args, 0, (hipStream_t)stream);
+        hipLaunchKernel(fn, dim3(8 * ((items + 7) / 8)), dim3(pcpa::tile_threads(p->head_dim, false)), args, 0,
+                        (hipStream_t)stream);
     return err == hipSuccess ? PCPA_OK : PCPA_ERR_LAUNCH;
 }
 

@@ -26,16 +26,31 @@ struct TileShape {
     static constexpr int NBUF = (!WIDEN && 4 * TILE <= 131072) ? 2 : 1;
     static constexpr int QK = FP8 ? D / 64 : D / 16;   // k-steps of the score MFMA
     static constexpr int DT = D / 32;                  // 32-row d tiles of O^T
-    static constexpr int DMA_PER_WAVE = CHUNKS / 4;    // 1 KB DMA blocks per wave per operand
-    // Wave w loads DMA blocks 4i + w.  Block i's lane chunk sits DMA_ROW_DELTA(i)
-    // key rows after block 0's, with the same chunk swizzle, except for 512-byte
-    // rows (bf16 D=256) whose swizzle changes between blocks: those keep one
-    // offset per block (DMA_SPLIT).
-    static constexpr bool DMA_SPLIT = ROW == 512;
+    // BF16 MFMAs at head_dim 256 run eight waves in key-split pairs: the two
+    // waves of a SIMD take the same 32 rows and one half of every tile's
+    // keys each, with an online softmax and O^T of their own, merged
+    // through LDS at the end.  (One wave holding all 64 keys of a tile
+    // needs 448 registers, i.e. one wave per SIMD and nothing to overlap
+    // the softmax with.)
+    static constexpr bool PAIR = D == 256 && !FP8;
+    static constexpr int WAVES = PAIR ? 2 * kWaves : kWaves;
+    static constexpr int THREADS = 64 * WAVES;
+    static constexpr int NT = PAIR ? 1 : 2;            // 32-key score tiles per wave and tile
+    static constexpr int DMA_PER_WAVE = CHUNKS / WAVES;  // 1 KB DMA blocks per wave per operand
+    // LDS: the tile buffers, which a PAIR workgroup reuses for the partners'
+    // O^T (32 KB per pair) after the walk.
+    static constexpr int LDS_BYTES = (PAIR && NBUF * 2 * TILE < 4 * 32768) ? 4 * 32768 : NBUF * 2 * TILE;
+    // Wave w loads DMA blocks WAVES i + w.  Block i's lane chunk sits
+    // dma_key_delta(i) key rows after block 0's, with the same chunk swizzle,
+    // except for 512-byte rows (bf16 D=256) loaded by four waves, whose
+    // blocks are 8 rows apart and whose swizzle (a function of the row mod
+    // 16) changes between blocks: those keep one offset per block
+    // (DMA_SPLIT).  Eight waves put a wave's blocks 16 rows apart.
+    static constexpr bool DMA_SPLIT = ROW == 512 && WAVES == kWaves;
     static constexpr int K_T1_ROWS = FP8 ? 16 : 32;    // LDS rows from score tile 0 to tile 1
     static constexpr int dma_key_delta(int i) {
-        // keys between DMA block i's lane chunk and block 0's (rows are 4i*1024/ROW apart)
-        return FP8 ? (ROW == 256 ? 16 * (i & 1) + 8 * (i >> 1) : ROW == 128 ? 8 * i : 0) : i * 4096 / ROW;
+        // keys between DMA block i's lane chunk and block 0's (rows are WAVES i 1024 / ROW apart)
+        return FP8 ? (ROW == 256 ? 16 * (i & 1) + 8 * (i >> 1) : ROW == 128 ? 8 * i : 0) : i * WAVES * 1024 / ROW;
     }
     // Lazy rescale: the running max is only raised when a tile's max exceeds
     // it by more than this (log2 units); FP8 probabilities then stay below
@@ -43,8 +58,13 @@ struct TileShape {
     static constexpr float RESCALE_LOG2 = FP8 ? 2.5f : 8.0f;
     // BF16 MFMAs at head_dim 256 (one wave per SIMD) hold O^T in the
     // accumulation registers for the whole walk.
-    static constexpr bool ACC_RESIDENT = D == 256 && !FP8;
+    static constexpr bool ACC_RESIDENT = D == 256 && !FP8 && !PAIR;
 };
+
+// Threads per workgroup of the tile kernel for a head dim and MFMA precision.
+__host__ __device__ constexpr int tile_threads(int d, bool fp8) {
+    return (d == 256 && !fp8) ? TileShape<256, false, false>::THREADS : kThreads;
+}
 
 // Per-lane constants of the main loop (LDS offsets are within one buffer).
 template <class S>
@@ -69,12 +89,12 @@ __device__ __forceinline__ void stage_tile_async(const FwdArgs& a, const TileCur
     uint8_t* const lk = lds + BUF * 2 * S::TILE;
 #pragma unroll
     for (int i = 0; i < S::DMA_PER_WAVE; ++i) {
-        const int block = 4 * i + wave;
+        const int block = S::WAVES * i + wave;
         const uint32_t koff = L.dma_off[S::DMA_SPLIT ? i : 0];
         const uint32_t voff = L.dma_off_v[S::DMA_SPLIT ? i : 0];
         const int delta = S::DMA_SPLIT ? 0 : S::dma_key_delta(i) * S::GROW;
-        __builtin_amdgcn_global_load_lds(kt + delta + koff, PCPA_LDS(void, lk + block * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vt + delta + voff, PCPA_LDS(void, lk + S::TILE + block * 1024), 16, 0, 0);
+        dma_sbase<0>(kt + delta, koff, lds_address(lk + block * 1024));
+        dma_sbase<0>(vt + delta, voff, lds_address(lk + S::TILE + block * 1024));
     }
 }
 
@@ -83,15 +103,15 @@ __device__ __forceinline__ void stage_tile_async(const FwdArgs& a, const TileCur
 template <class S>
 __device__ __forceinline__ void stage_tile_sync(const FwdArgs& a, const TileCursor& c, int valid, uint8_t* lds,
                                                 int tid) {
-    constexpr int LOADS = kKeyTile * S::GROW / (16 * kThreads);
-    static_assert((kKeyTile * S::GROW) % (16 * kThreads) == 0, "tile must split into 16-byte chunks per thread");
+    constexpr int LOADS = kKeyTile * S::GROW / (16 * S::THREADS);
+    static_assert((kKeyTile * S::GROW) % (16 * S::THREADS) == 0, "tile must split into 16-byte chunks per thread");
     const uint8_t* const kpage = a.kv + c.k_off;
     const uint8_t* const vpage = kpage + (int64_t)a.num_kv_heads * a.head_stride;
     uint8_t* const lds_k = lds;
     uint8_t* const lds_v = lds + S::TILE;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-        const int chunk_id = tid + kThreads * i;
+        const int chunk_id = tid + S::THREADS * i;
         const int key = chunk_id / S::GCHUNKS;
         const int ch = chunk_id - key * S::GCHUNKS;
         const int64_t goff = (int64_t)(c.base + key) * S::GROW + ch * 16;
@@ -124,7 +144,7 @@ __device__ __forceinline__ void stage_tile_sync(const FwdArgs& a, const TileCurs
 // keys cannot inject NaN bit patterns from unused cache slots.
 template <class S>
 __device__ __forceinline__ void zero_masked_v(uint8_t* lds_v, int valid, int tid) {
-    for (int idx = tid; idx < (kKeyTile - valid) * S::CHUNKS; idx += kThreads) {
+    for (int idx = tid; idx < (kKeyTile - valid) * S::CHUNKS; idx += S::THREADS) {
         const int key = valid + idx / S::CHUNKS;
         *(v4i*)(lds_v + lds_row<S::ES == 1>(key) * S::ROW + (idx % S::CHUNKS) * 16) = v4i{0, 0, 0, 0};
     }
@@ -143,18 +163,25 @@ struct SoftmaxState {
 template <class S>
 using QOperand = typename std::conditional<S::ES == 1, v8i, v8bf>::type;
 
-// One 64-key tile held in LDS buffer BUF: S^T = K Q^T, masked online
-// softmax, O^T += V^T P^T.
+// One 64-key tile held in LDS buffer BUF (PAIR: this wave's 32 keys of it;
+// its operand addresses in L include the half): S^T = K Q^T, masked online
+// softmax, O^T += V^T P^T.  `valid`: the valid keys counted from the wave's
+// first key.
 // CAUSAL: `valid` differs per lane (the row's causal limit within the tile,
 // possibly <= 0).
+//
+// rt_off: a byte offset added to both buffers' addresses at run time (PAIR
+// walks alternate buffers with one loop body, BUF 0 and rt_off 0 or
+// 2 * TILE; otherwise 0).
 template <class S, int BUF, bool CAUSAL = false>
-__device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, const QOperand<S> (&qop)[S::QK],
-                                             float cscale, const LaneMap<S>& L, int h, SoftmaxState<S>& st) {
+__device__ __forceinline__ void compute_tile(const uint8_t* lds, uint32_t rt_off, int valid,
+                                             const QOperand<S> (&qop)[S::QK], float cscale, const LaneMap<S>& L, int h,
+                                             SoftmaxState<S>& st) {
     constexpr bool FP8 = S::ES == 1;
     constexpr int ROW = S::ROW, QK = S::QK, DT = S::DT;
     constexpr int KBASE = BUF * 2 * S::TILE;
     constexpr int VBASE = KBASE + S::TILE;
-    const uint8_t* const lk = lds + KBASE;
+    const uint8_t* const lk = lds + KBASE + rt_off;
 
     // ---- S^T = K . Q^T : two 32-key x 32-query tiles --------------------
     v16f s[2];
@@ -178,7 +205,7 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
         v4i kb[2][2];
         auto load = [&](v4i (&k)[2], int c) {
             k[0] = *(const v4i*)(lk + (L.k_addr ^ ((2 * c) << 4)));
-            k[1] = *(const v4i*)(kt1 + (L.k_addr ^ ((2 * c) << 4)));
+            if constexpr (S::NT > 1) k[1] = *(const v4i*)(kt1 + (L.k_addr ^ ((2 * c) << 4)));
         };
         s[0] = v16f{};
         s[1] = v16f{};
@@ -189,7 +216,7 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
             // (the barriers keep the reads of step c + 1 ahead of step c's MFMAs)
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < S::NT; ++t)
                 s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, kb[c & 1][t]), qop[c], s[t], 0,
                                                                0, 0);
             __builtin_amdgcn_sched_barrier(0);
@@ -198,12 +225,13 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
 
     // ---- mask, online softmax (lazy rescale) ----------------------------
     // (CAUSAL: only tiles that cross some row's limit, a wave-uniform test)
-    if (CAUSAL ? __builtin_amdgcn_ballot_w64(valid < kKeyTile) != 0 : valid < kKeyTile) {
+    constexpr int KEYS = 32 * S::NT;  // keys of the tile this wave scores
+    if (CAUSAL ? __builtin_amdgcn_ballot_w64(valid < KEYS) != 0 : valid < KEYS) {
         // key_of_acc(t, r, h) >= valid, as its lane-independent part against
         // valid less its lane-half part
         const int lim = valid - key_of_acc<FP8>(0, 0, h);
         const float ninf = -INFINITY;
-        static_for<0, 32>([&](auto kc) {
+        static_for<0, 16 * S::NT>([&](auto kc) {
             constexpr int t = decltype(kc)::value >> 4, r = decltype(kc)::value & 15;
             constexpr int k = FP8 ? 16 * t + r : 32 * t + 16 * (r >> 3) + (r & 7);
             s[t][r] = mask_key_at_or_past<k>(s[t][r], lim, ninf);
@@ -211,7 +239,7 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < S::NT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
     const float mxs = halves_max(mx) * cscale;
@@ -255,7 +283,7 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
     float psum = 0.f;
     const float shift = (FP8 ? kPBiasLog2 : 0.f) - st.m;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < S::NT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], cscale, shift));
@@ -330,7 +358,7 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
     } else {
         v8bf pop[2][2];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < S::NT; ++t)
 #pragma unroll
             for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -343,13 +371,38 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
         // The second buffer of a 32 KB tile lies beyond the 16-bit immediate:
         // its 64 KB part goes into the address.
         constexpr uint32_t VHI = VBASE & ~0xFFFFu;
-        constexpr int STEPS = 2 * DT;
+        if constexpr (S::PAIR) {
+            // One wave's 32 keys: per d tile two MFMAs (keys 0-15, 16-31 of
+            // its half), each operand's two reads issued one MFMA ahead (two
+            // 4-register buffers: this mode has no registers for more).
+            constexpr int SUB = 2 * DT;
+            v2i vb[2][2];
+            auto issue1 = [&](auto sc) {
+                constexpr int sub = decltype(sc)::value, dt = sub >> 1, u = sub & 1;
+                constexpr int o = (VBASE + 16 * u * ROW) & 0xFFFF;
+                vb[sub & 1][0] = ds_read_tr16_b64<o>((L.v_addr[0] ^ ((4 * dt) << 4)) + (VHI + rt_off));
+                vb[sub & 1][1] = ds_read_tr16_b64<o>((L.v_addr[1] ^ ((4 * dt) << 4)) + (VHI + rt_off));
+            };
+            issue1(std::integral_constant<int, 0>{});
+            static_for<0, SUB>([&](auto sc) {
+                constexpr int sub = decltype(sc)::value, dt = sub >> 1, u = sub & 1;
+                v2i(&x)[2] = vb[sub & 1];
+                lds_results_ready(x);
+                if constexpr (sub + 1 < SUB) issue1(std::integral_constant<int, sub + 1>{});
+                __builtin_amdgcn_sched_barrier(0);
+                const v4i aop = {x[0][0], x[0][1], x[1][0], x[1][1]};
+                st.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, aop), pop[0][u], st.o[dt], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+            return;
+        }
+        constexpr int STEPS = S::NT * DT;
         v2i buf[2][4];
         auto issue = [&](auto sc) {
-            constexpr int step = decltype(sc)::value, dt = step >> 1, t = step & 1;
+            constexpr int step = decltype(sc)::value, dt = step / S::NT, t = step % S::NT;
             constexpr int o0 = (VBASE + 32 * t * ROW) & 0xFFFF, o1 = (VBASE + (32 * t + 16) * ROW) & 0xFFFF;
-            const uint32_t a0 = (L.v_addr[0] ^ ((4 * dt) << 4)) + VHI;
-            const uint32_t a1 = (L.v_addr[1] ^ ((4 * dt) << 4)) + VHI;
+            const uint32_t a0 = (L.v_addr[0] ^ ((4 * dt) << 4)) + (VHI + rt_off);
+            const uint32_t a1 = (L.v_addr[1] ^ ((4 * dt) << 4)) + (VHI + rt_off);
             v2i(&x)[4] = buf[step & 1];
             x[0] = ds_read_tr16_b64<o0>(a0);
             x[1] = ds_read_tr16_b64<o0>(a1);
@@ -358,7 +411,7 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
         };
         issue(std::integral_constant<int, 0>{});
         static_for<0, STEPS>([&](auto sc) {
-            constexpr int step = decltype(sc)::value, dt = step >> 1, t = step & 1;
+            constexpr int step = decltype(sc)::value, dt = step / S::NT, t = step % S::NT;
             v2i(&x)[4] = buf[step & 1];
             lds_results_ready(x);
             if constexpr (step + 1 < STEPS) issue(std::integral_constant<int, step + 1>{});
@@ -375,17 +428,26 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, int valid, cons
 
 // Wait for tile `cur` (in BUF), start the prefetch of `nxt` into the other
 // buffer, then compute `cur`.
+// PAIR (double-buffered): BUF is 0 and rbuf the buffer of `cur`, so that
+// the walk has one loop body (two bodies made the register allocator keep
+// copies of O^T across them and spill).
 template <class S, int BUF, bool CAUSAL>
 __device__ __forceinline__ void tile_step(const FwdArgs& a, const TileCursor& cur, const TileCursor& nxt,
                                           uint8_t* lds, int wave, int tid, int h, const LaneMap<S>& L,
                                           const QOperand<S> (&qop)[S::QK], float cscale, SoftmaxState<S>& st,
-                                          int row_limit) {
+                                          int row_limit, int first_key, int rbuf) {
     const int valid = min(kKeyTile, cur.n - cur.base);
-    uint8_t* const lds_v = lds + BUF * 2 * S::TILE + S::TILE;
+    const uint32_t rt_off = S::PAIR && S::NBUF == 2 ? rbuf * 2 * S::TILE : 0;
+    uint8_t* const lds_v = lds + BUF * 2 * S::TILE + rt_off + S::TILE;
     if constexpr (S::NBUF == 2) {
         wait_vmem();      // this wave's loads of the current tile have landed
         __syncthreads();  // ... and every wave's; the other buffer is free
-        if (nxt.e < a.num_entries) stage_tile_async<S, BUF ^ 1>(a, nxt, lds, wave, L);
+        if (nxt.e < a.num_entries) {
+            if constexpr (S::PAIR)
+                stage_tile_async<S, 0>(a, nxt, lds + (rt_off ^ (2 * S::TILE)), wave, L);
+            else
+                stage_tile_async<S, BUF ^ 1>(a, nxt, lds, wave, L);
+        }
         if (valid < kKeyTile) {
             zero_masked_v<S>(lds_v, valid, tid);
             __syncthreads();
@@ -402,7 +464,36 @@ __device__ __forceinline__ void tile_step(const FwdArgs& a, const TileCursor& cu
         }
         __syncthreads();
     }
-    compute_tile<S, BUF, CAUSAL>(lds, CAUSAL ? min(valid, row_limit - cur.base) : valid, qop, cscale, L, h, st);
+    compute_tile<S, BUF, CAUSAL>(lds, rt_off, (CAUSAL ? min(valid, row_limit - cur.base) : valid) - first_key, qop,
+                                 cscale, L, h, st);
+}
+
+// Query row of lane j of the wave in 32-row slot pw: its index among the
+// KV head's rows (FIXUP: the plan's gathered row, -1 for padding), whether
+// it exists, its rank and local token, and the byte offset of its Q and
+// output rows in [pcp, Hq, local_q, D] bf16.
+struct QueryRow {
+    int row;
+    bool ok;
+    int rank;
+    int tok;
+    int64_t off;
+};
+template <int D, bool FIXUP>
+__device__ __forceinline__ QueryRow query_row(const FwdArgs& a, int head, int slot, int row_tile, int pw, int j) {
+    QueryRow r;
+    if constexpr (FIXUP)
+        r.row = a.guard_plan[guard_list_offset(a.num_kv_heads) + slot * kRowsPerGroup + pw * kRowsPerWave + j];
+    else
+        r.row = row_tile * kRowsPerGroup + pw * kRowsPerWave + j;
+    r.ok = FIXUP ? r.row >= 0 : r.row < a.rows_per_head;
+    const int rowc = r.ok ? r.row : (FIXUP ? 0 : a.rows_per_head - 1);
+    r.rank = rowc / a.group_rows;
+    const int rem = rowc - r.rank * a.group_rows;
+    const int head_in_group = rem / a.local_q;
+    r.tok = rem - head_in_group * a.local_q;
+    r.off = ((int64_t)(r.rank * a.num_q_heads + head * a.group + head_in_group) * a.local_q + r.tok) * D * 2;
+    return r;
 }
 
 // CAUSAL: causal attention of the current tokens among themselves (their
@@ -420,14 +511,16 @@ __device__ __forceinline__ void tile_step(const FwdArgs& a, const TileCursor& cu
 // guard_merge_kernel), in dense mode it takes group b and writes the output
 // directly; workgroups past the plan exit at once.
 template <int D, bool STORE8, bool FP8, bool CAUSAL = false, bool SPLIT = false, bool FIXUP = false>
-__global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_fwd_kernel(FwdArgs a) {
+__global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileShape<D, STORE8, FP8>::PAIR ? 1 : 2))
+    history_fwd_kernel(FwdArgs a) {
     static_assert(!(CAUSAL && SPLIT), "the current-token step is not split");
     static_assert(!FIXUP || (!FP8 && !CAUSAL && !SPLIT), "the guard's fixup runs BF16 MFMAs, one launch");
     using S = TileShape<D, STORE8, FP8>;
     constexpr int ROW = S::ROW, CHUNKS = S::CHUNKS, QK = S::QK, DT = S::DT;
 
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[S::NBUF * 2 * S::TILE];
-    __shared__ int wave_limit[kWaves];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S::LDS_BYTES];
+    __shared__ int wave_limit[S::WAVES];
+    __shared__ float pair_ml[S::PAIR ? kWaves * 64 * 2 : 1];  // PAIR: the partners' (m, l) per lane
 
     // ---- XCD-aware work mapping ------------------------------------------
     // Workgroups are dealt to the 8 XCDs round-robin by launch index; give
@@ -489,27 +582,19 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // PAIR: waves w and w + 4 (one SIMD) share 32 rows; wave w + 4 takes the
+    // tiles' keys 32..63
+    const int pw = S::PAIR ? wave & (kWaves - 1) : wave;  // the wave's 32-row slot
+    const int kh = S::PAIR ? wave / kWaves : 0;           // its key half
     const int j = lane & 31;  // query column of the score tile / A-operand row
     const int h = lane >> 5;  // k-group (lane half)
     const int grp = lane >> 4;
     const int gl = lane & 15;
 
     // ---- this lane's query row -------------------------------------------
-    // (FIXUP: the plan's gathered row of the head, -1 for padding)
-    int row;
-    if constexpr (FIXUP)
-        row = a.guard_plan[guard_list_offset(a.num_kv_heads) + slot * kRowsPerGroup + wave * kRowsPerWave + j];
-    else
-        row = row_tile * kRowsPerGroup + wave * kRowsPerWave + j;
-    const bool row_ok = FIXUP ? row >= 0 : row < a.rows_per_head;
-    const int rowc = row_ok ? row : (FIXUP ? 0 : a.rows_per_head - 1);
-    const int rank = rowc / a.group_rows;
-    const int rem = rowc - rank * a.group_rows;
-    const int head_in_group = rem / a.local_q;
-    const int tok = rem - head_in_group * a.local_q;
-    const int64_t row_off =
-        ((int64_t)(rank * a.num_q_heads + head * a.group + head_in_group) * a.local_q + tok) * D * 2;
-    const uint8_t* const qrow = a.q + row_off;
+    const QueryRow qr = query_row<D, FIXUP>(a, head, slot, row_tile, pw, j);
+    const int rank = qr.rank, tok = qr.tok;
+    const uint8_t* const qrow = a.q + qr.off;
 
     // ---- Q^T operand (register resident for the whole history) ------------
     QOperand<S> qop[QK];
@@ -567,24 +652,26 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
     {
         const int row = lds_row<FP8>(key_of_row<FP8>(0, j));
         const int first_chunk = FP8 ? 2 * h : h;
-        L.k_addr = row * ROW + ((first_chunk ^ chunk_swizzle<FP8, CHUNKS>(row)) << 4);
+        L.k_addr = row * ROW + ((first_chunk ^ chunk_swizzle<FP8, CHUNKS>(row)) << 4) + kh * S::K_T1_ROWS * ROW;
     }
     if constexpr (FP8) {
         // key 32*(grp>>1) + (gl>>1) (+ 8s for the other reads) -> row below
         const int row = lds_row<FP8>(32 * (grp >> 1) + (gl >> 1));
-        L.v_addr[0] = row * ROW + (((grp & 1) ^ chunk_swizzle_v<FP8, CHUNKS>(row)) << 4) + 8 * (gl & 1);
+        L.v_addr[0] = lds_address(lds) + row * ROW + (((grp & 1) ^ chunk_swizzle_v<FP8, CHUNKS>(row)) << 4) +
+                      8 * (gl & 1);
         L.rsel = ((lane ^ (lane >> 2)) & 4) ? 0 : 0x38383838;
     } else {
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
             const int vkey = 8 * (grp >> 1) + 4 * s2 + (gl >> 2);  // + 16u + 32t: same swizzle
             const int dbyte = 2 * (16 * (grp & 1) + 4 * (gl & 3));
-            L.v_addr[s2] = vkey * ROW + (((dbyte >> 4) ^ chunk_swizzle<FP8, CHUNKS>(vkey)) << 4) + (dbyte & 15);
+            L.v_addr[s2] = lds_address(lds) + vkey * ROW + (((dbyte >> 4) ^ chunk_swizzle<FP8, CHUNKS>(vkey)) << 4) +
+                           (dbyte & 15) + kh * 32 * ROW;
         }
     }
 #pragma unroll
     for (int i = 0; i < (S::DMA_SPLIT ? S::DMA_PER_WAVE : 1); ++i) {
-        const int byte = (4 * i + wave) * 1024 + lane * 16;
+        const int byte = (S::WAVES * i + wave) * 1024 + lane * 16;
         const int row = byte / ROW;
         const int pos = (byte % ROW) / 16;
         L.dma_off[i] = lds_row<FP8>(row) * S::GROW + (pos ^ chunk_swizzle<FP8, CHUNKS>(row)) * 16;
@@ -593,7 +680,11 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
 
     // ---- walk the block table -----------------------------------------------
     SoftmaxState<S> st;
-    st.m = -INFINITY;
+    // PAIR: a wave can see a whole tile masked before any valid key (its
+    // half of a row's first tile); a finite floor keeps the probabilities of
+    // such a tile 0 (2^(-inf + 1e30)) instead of NaN (2^(-inf + inf)), and
+    // the first real tile rescales by 2^(-1e30 - m) = 0.
+    st.m = S::PAIR ? -1.0e30f : -INFINITY;
     st.l = 0.f;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) st.o[dt] = v16f{};
@@ -611,7 +702,7 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
         __syncthreads();
         group_limit = wave_limit[0];
 #pragma unroll
-        for (int i = 1; i < kWaves; ++i) group_limit = max(group_limit, wave_limit[i]);
+        for (int i = 1; i < S::WAVES; ++i) group_limit = max(group_limit, wave_limit[i]);
     }
     auto advance = [&](const TileCursor& c) {
         if constexpr (CAUSAL) {
@@ -631,20 +722,65 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
     if constexpr (S::NBUF == 2) {
         if (cur.e < a.num_entries) stage_tile_async<S, 0>(a, cur, lds, wave, L);
     }
-    while (cur.e < a.num_entries) {
-        TileCursor nxt = advance(cur);
-        tile_step<S, 0, CAUSAL>(a, cur, nxt, lds, wave, tid, h, L, qop, cscale, st, row_limit);
-        cur = nxt;
-        if constexpr (S::NBUF == 2) {
-            if (cur.e >= a.num_entries) break;
-            nxt = advance(cur);
-            tile_step<S, 1, CAUSAL>(a, cur, nxt, lds, wave, tid, h, L, qop, cscale, st, row_limit);
+    if constexpr (S::PAIR && S::NBUF == 2) {
+        for (int rbuf = 0; cur.e < a.num_entries; rbuf ^= 1) {
+            const TileCursor nxt = advance(cur);
+            tile_step<S, 0, CAUSAL>(a, cur, nxt, lds, wave, tid, h, L, qop, cscale, st, row_limit, 32 * kh, rbuf);
             cur = nxt;
         }
+    } else {
+        while (cur.e < a.num_entries) {
+            TileCursor nxt = advance(cur);
+            tile_step<S, 0, CAUSAL>(a, cur, nxt, lds, wave, tid, h, L, qop, cscale, st, row_limit, 32 * kh, 0);
+            cur = nxt;
+            if constexpr (S::NBUF == 2) {
+                if (cur.e >= a.num_entries) break;
+                nxt = advance(cur);
+                tile_step<S, 1, CAUSAL>(a, cur, nxt, lds, wave, tid, h, L, qop, cscale, st, row_limit, 32 * kh, 0);
+                cur = nxt;
+            }
+        }
+    }
+
+    // ---- PAIR: the key halves' results meet in the first wave of the pair --
+    if constexpr (S::PAIR) {
+        // O^T as [pair][register quad][lane] float4s (conflict-free), m and
+        // this lane half's l beside; (m, l) = (-1e30, 0) for a half that saw
+        // no valid key (weight 2^(-1e30 - m) = 0 against a real m).
+        float* const xo = (float*)lds + pw * (DT * 16 * 64);
+        __syncthreads();  // every wave is done with the tile buffers
+        if (kh == 1) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    *(v4f*)(xo + ((4 * dt + r4) * 64 + lane) * 4) =
+                        v4f{st.o[dt][4 * r4], st.o[dt][4 * r4 + 1], st.o[dt][4 * r4 + 2], st.o[dt][4 * r4 + 3]};
+            pair_ml[(pw * 64 + lane) * 2] = st.m;
+            pair_ml[(pw * 64 + lane) * 2 + 1] = st.l;
+        }
+        __syncthreads();
+        if (kh == 1) return;
+        const float m1 = pair_ml[(pw * 64 + lane) * 2], l1 = pair_ml[(pw * 64 + lane) * 2 + 1];
+        const float m = fmaxf(st.m, m1);
+        const float w0 = __builtin_amdgcn_exp2f(st.m - m), w1 = __builtin_amdgcn_exp2f(m1 - m);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const v4f x = *(const v4f*)(xo + ((4 * dt + r4) * 64 + lane) * 4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) st.o[dt][4 * r4 + i] = fmaf(w1, x[i], w0 * st.o[dt][4 * r4 + i]);
+            }
+        st.l = fmaf(w1, l1, w0 * st.l);
+        st.m = m;
     }
 
     // ---- epilogue: O = O^T / l, bf16; log-sum-exp; merge -------------------
     // (FP8: st.l is already the whole row's sum, in both lane halves)
+    const QueryRow er = qr;
+    const bool row_ok = er.ok;
+    const int64_t row_off = er.off;
     const float l_tot = FP8 ? st.l : halves_sum(st.l);
     float scale = l_tot > 0.f ? a.v_scale / l_tot : 0.f;
     // sum_k exp(score_k) = l * 2^(m - bias): P was 2^(x - m + bias)
@@ -654,7 +790,7 @@ __global__ void __launch_bounds__(kThreads, (D == 256 && !FP8) ? 1 : 2) history_
         // guard partials [splits, slots * 128, D]: slot rows in tile order
         if (row_ok) {
             const int64_t prow = (int64_t)split * a.guard_slots * kRowsPerGroup + (int64_t)slot * kRowsPerGroup +
-                                 wave * kRowsPerWave + j;
+                                 pw * kRowsPerWave + j;
             float* const po = a.part_o + prow * D;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt)

@@ -1,9 +1,11 @@
 """Properties of the compiled gfx950 device code (CPU only: hipcc cross-compiles).
 
-* No attention kernel spills to scratch: a Q fragment reloaded from scratch
-  inside the walk cost 30% on the MI355X (8.87 against 6.8 ms on the full
-  64-rank workload; the reload's vmcnt wait also waits for every LDS-DMA in
-  flight).
+* No attention kernel spills to scratch, except the BF16 head_dim-256 tile
+  kernels (eight waves in key-split pairs, 256 registers a wave), whose few
+  spills (values the epilogue needs from the prologue) must stay outside
+  every loop: a Q fragment reloaded from scratch inside the walk cost 30% on
+  the MI355X (8.87 against 6.8 ms on the full 64-rank workload; the reload's
+  vmcnt wait also waits for every LDS-DMA in flight).
 * No LDS read writes a register that an MFMA issued before it is still
   going to write.  The transposing V reads and the score-operand reads are
   inline asm, invisible to the compiler's hazard checks; the kernels keep
@@ -57,6 +59,11 @@ def _attention_kernels(usage):
     return names
 
 
+def _is_pair_tile(name):
+    # history_fwd_kernel<256, STORE8, FP8 = false, ...>: the key-split pair mode
+    return re.search(r"history_fwd_kernelILi256ELb[01]ELb0E", name) is not None
+
+
 def _is_split_overlap(name):
     # history_fwd_overlap<D, FAST, LSE, SPLIT = true>
     return "history_fwd_overlap" in name and name.endswith("ELb1EEEvNS_7FwdArgsE")
@@ -78,10 +85,14 @@ def test_attention_kernels_do_not_spill(device_code):
     usage, _ = device_code
     split = [n for n in _attention_kernels(usage) if _is_split_overlap(n)]
     assert len(split) == 2, split  # the split instantiations (fast and exact exp2) are covered too
+    pair = [n for n in _attention_kernels(usage) if _is_pair_tile(n)]
+    assert len(pair) == 6, pair  # BF16 and widened caches: one pass, split, guard fixup, current step
     for name in _attention_kernels(usage):
-        assert usage[name].get("ScratchSize", -1) == 0, (name, usage[name])
-        assert usage[name].get("VGPRs Spill", -1) == 0, (name, usage[name])
+        limit = 128 if _is_pair_tile(name) else 0
+        assert 0 <= usage[name].get("ScratchSize", -1) <= limit, (name, usage[name])
         assert usage[name].get("SGPRs Spill", -1) == 0, (name, usage[name])
+        if not limit:
+            assert usage[name].get("VGPRs Spill", -1) == 0, (name, usage[name])
 
 
 def test_no_scratch_access_inside_any_loop(device_code):
