@@ -56,9 +56,6 @@ struct TileShape {
     // it by more than this (log2 units); FP8 probabilities then stay below
     // 2^(kPBiasLog2 + 2.5) = 362 < 448.
     static constexpr float RESCALE_LOG2 = FP8 ? 2.5f : 8.0f;
-    // BF16 MFMAs at head_dim 256 (one wave per SIMD) hold O^T in the
-    // accumulation registers for the whole walk.
-    static constexpr bool ACC_RESIDENT = D == 256 && !FP8 && !PAIR;
 };
 
 // Threads per workgroup of the tile kernel for a head dim and MFMA precision.
@@ -247,37 +244,8 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, uint32_t rt_off
         const float m_new = fmaxf(st.m, mxs);
         const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
         st.l *= alpha;
-        if constexpr (S::ACC_RESIDENT) {
-            // O^T stays in the accumulation registers: read, scale and write
-            // back each one in place, so that no loop-carried copy of O^T is
-            // kept in VGPRs (the compiler otherwise copied all 128 registers
-            // out of and back into AGPRs on every tile).  The first read
-            // waits 24 cycles for the last PV MFMA's results (a 16-pass
-            // MFMA's results are readable after 18); the last write is
-            // followed by 5 before the next MFMA may read it.
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float x = st.o[dt][r];
-                    float t;
-                    if (dt == 0 && r == 0)
-                        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\t"
-                                     "v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
-                                     : "+a"(x), "=&v"(t) : "v"(alpha));
-                    else if (dt == DT - 1 && r == 15)
-                        asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1\n\t"
-                                     "s_nop 4"
-                                     : "+a"(x), "=&v"(t) : "v"(alpha));
-                    else
-                        asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
-                                     : "+a"(x), "=&v"(t) : "v"(alpha));
-                    st.o[dt][r] = x;
-                }
-        } else {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) st.o[dt] *= alpha;
-        }
+        for (int dt = 0; dt < DT; ++dt) st.o[dt] *= alpha;
         st.m = m_new;
     }
     float psum = 0.f;
