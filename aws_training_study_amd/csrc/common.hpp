@@ -144,22 +144,37 @@ __host__ __device__ __forceinline__ constexpr int lds_row(int key) {
 }
 
 // XOR swizzle of the 16-byte chunk index within LDS row `row`, making the
-// score-operand reads (16 rows per 16-lane group) and the transposing V
-// reads (8 rows x 16 bytes, or 4 rows x 32 bytes) bank-conflict free.
+// score-operand reads (ds_read_b128, 16 rows per 16-lane group) and the
+// transposing V reads bank-conflict free (measured with the LDS
+// bank-conflict counter on gfx950, per read pattern).  BF16 rows of 128
+// bytes (head_dim 64) sit in alternate halves of the 64 banks, so their K
+// swizzle spreads even and odd rows over all 8 chunks each.
 template <bool FP8, int CHUNKS>
 __device__ __forceinline__ int chunk_swizzle(int row) {
     constexpr int mask = (CHUNKS < 16 ? CHUNKS : 16) - 1;
-    const int s = FP8 ? (row & 15) : (((row & 7) << 1) | ((row >> 3) & 1));
-    return s & mask;
+    if constexpr (FP8) return row & 15 & mask;
+    if constexpr (CHUNKS == 8) return (row >> 1) & 7;
+    return (((row & 7) << 1) | ((row >> 3) & 1)) & mask;
 }
 // FP8 V tiles use an even-only swizzle: the two 16-lane groups of a
 // transposing read that share rows (d halves 2dt and 2dt+1) then land on
 // disjoint chunk sets (even vs odd), so 32 lanes cover all 64 banks once.
+// BF16 V tiles of 256-byte rows (head_dim 128): a 32-lane transposing read
+// covers 4 consecutive rows x 4 chunks, and rows 4s and 4s + 1 (4s + 2 and
+// 4s + 3) would share their chunk block under the score swizzle (2-way
+// conflicts, 1.8 extra cycles per read); flipping chunk bit 3 on odd rows
+// separates them (GQA-8 workload 1.99 -> 1.97 ms).  Other BF16 rows keep
+// the score operand's former swizzle: 128-byte rows are conflict-free with
+// it, and for 512-byte rows (head_dim 256, key-split pairs) the flip
+// measured slower (the extra lane-address work costs more than the
+// conflicts, which the partner wave hides).
 template <bool FP8, int CHUNKS>
 __device__ __forceinline__ int chunk_swizzle_v(int row) {
     constexpr int mask = (CHUNKS < 16 ? CHUNKS : 16) - 1;
     if constexpr (FP8) return (2 * row) & mask & 14;
-    return chunk_swizzle<FP8, CHUNKS>(row);
+    const int s = (((row & 7) << 1) | ((row >> 3) & 1)) & mask;
+    if constexpr (CHUNKS == 16) return s ^ ((row & 1) << 3);
+    return s;
 }
 
 // s = -inf unless K < lim, through vcc alone.  Written as plain C++ over a

@@ -124,12 +124,15 @@ __device__ __forceinline__ void stage_tile_sync(const FwdArgs& a, const TileCurs
             const v2i k2 = e4m3x4_to_bf16x4(kc[2]), k3 = e4m3x4_to_bf16x4(kc[3]);
             const v2i v0 = e4m3x4_to_bf16x4(vc[0]), v1 = e4m3x4_to_bf16x4(vc[1]);
             const v2i v2 = e4m3x4_to_bf16x4(vc[2]), v3 = e4m3x4_to_bf16x4(vc[3]);
+            // (K and V rows have swizzles of their own)
             const int lo = row * S::ROW + (((2 * ch) ^ sw) << 4);
             const int hi = row * S::ROW + (((2 * ch + 1) ^ sw) << 4);
+            const int lov = row * S::ROW + (((2 * ch) ^ swv) << 4);
+            const int hiv = row * S::ROW + (((2 * ch + 1) ^ swv) << 4);
             *(v4i*)(lds_k + lo) = v4i{k0[0], k0[1], k1[0], k1[1]};
             *(v4i*)(lds_k + hi) = v4i{k2[0], k2[1], k3[0], k3[1]};
-            *(v4i*)(lds_v + lo) = v4i{v0[0], v0[1], v1[0], v1[1]};
-            *(v4i*)(lds_v + hi) = v4i{v2[0], v2[1], v3[0], v3[1]};
+            *(v4i*)(lds_v + lov) = v4i{v0[0], v0[1], v1[0], v1[1]};
+            *(v4i*)(lds_v + hiv) = v4i{v2[0], v2[1], v3[0], v3[1]};
         } else {
             *(v4i*)(lds_k + row * S::ROW + ((ch ^ sw) << 4)) = kc;
             *(v4i*)(lds_v + row * S::ROW + ((ch ^ swv) << 4)) = vc;
@@ -633,7 +636,7 @@ __global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileSha
         for (int s2 = 0; s2 < 2; ++s2) {
             const int vkey = 8 * (grp >> 1) + 4 * s2 + (gl >> 2);  // + 16u + 32t: same swizzle
             const int dbyte = 2 * (16 * (grp & 1) + 4 * (gl & 3));
-            L.v_addr[s2] = lds_address(lds) + vkey * ROW + (((dbyte >> 4) ^ chunk_swizzle<FP8, CHUNKS>(vkey)) << 4) +
+            L.v_addr[s2] = lds_address(lds) + vkey * ROW + (((dbyte >> 4) ^ chunk_swizzle_v<FP8, CHUNKS>(vkey)) << 4) +
                            (dbyte & 15) + kh * 32 * ROW;
         }
     }
