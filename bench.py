@@ -313,6 +313,7 @@ def current_bench(args) -> int:
     achieved = flops / (kernel_ms * 1e-3) / 1e12
     peak = PEAK_TFLOPS["bfloat16"]
     history_flops = model_flops(cfg)
+    traffic, traffic_source = measured_traffic(f"{workload.name}/current")
     result = {
         "metric": "current-token causal attention + LSE merge TFLOP/s (BF16 MFMA), 1 GPU",
         "value": round(flops / (ms_per_step * 1e-3) / 1e12, 2),
@@ -331,7 +332,9 @@ def current_bench(args) -> int:
                    "kv_heads": cfg.num_kv_heads, "head_dim": cfg.head_dim, "interleave": cfg.interleave_size},
         "kernel_ms": _kernel_ms(kernel_ms, spread),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(achieved / peak, 4), "traffic": None,
+                     "frac": round(achieved / peak, 4),
+                     "traffic": round(traffic) if traffic is not None else None,
+                     "traffic_source": traffic_source,
                      "algorithmic_bytes": 2.0 * (3 * cfg.num_q_heads * cfg.current_len * cfg.head_dim
                                                  + 2 * cfg.num_kv_heads * cfg.current_len * cfg.head_dim)
                      + 2 * 4.0 * cfg.num_q_heads * cfg.current_len},
