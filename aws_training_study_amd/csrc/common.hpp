@@ -70,29 +70,91 @@ struct FwdArgs {
     float* part_lse;          // [splits, pcp * Hq * local_q]
     float* part_m;            // [splits, pcp * Hq * local_q]: each range's reference max (log2)
     // Precision guard of the e4m3-MFMA kernels.  guard_out (one byte per
-    // row, [pcp, Hq, local_q]): the e4m3 kernel (or the split merge) writes 1
-    // for a row whose probability mass sum_k 2^(x_k - m) is below
-    // guard_min_mass, else 0.
+    // row, [pcp, Hq, local_q]): the one-pass e4m3 kernel writes 1 for a row
+    // whose probability mass sum_k 2^(x_k - m) is below guard_min_mass, else
+    // 0.  A split launch instead sets the row counts of the guard plan
+    // guard_zero to 0 (workgroup 0), and its merge appends the rows.
     uint8_t* guard_out;
     float guard_min_mass;
+    int32_t* guard_zero;
     // The BF16 fixup of a guarded launch (history_fwd_kernel<..., FIXUP>):
-    // the plan of guard_plan_kernel (below) and, in sparse mode, the
-    // partials' capacity in 128-row groups (part_o / part_lse hold [splits,
-    // guard_slots * 128] rows).
+    // the guard plan (below) and the partials' capacity in 128-row groups
+    // (part_o / part_lse hold [splits, guard_slots * 128] rows): with at
+    // most guard_slots groups the fixup is sparse (each group's history walk
+    // split over `splits` workgroups, partials merged by guard_merge_kernel),
+    // with more it is dense (one workgroup per group, output written
+    // directly).
     const int32_t* guard_plan;
     int32_t guard_slots;
 };
 
-// Modes of a guard plan: no flagged row, few flagged rows (history split
-// across workgroups, partials merged), or many (one pass per group).
-constexpr int kGuardNone = 0;
-constexpr int kGuardSparse = 1;
-constexpr int kGuardDense = 2;
-// A plan: [0] 128-row groups, [1] mode, [2 + h] first group of KV head h
-// ([2 + num_kv_heads] = [0]), then, from guard_list_offset, the gathered
-// rows (head row indices, -1 padding), 128 per group.
-__host__ __device__ __forceinline__ int guard_list_offset(int num_kv_heads) {
-    return (2 + num_kv_heads + 1 + 3) / 4 * 4;
+// A guard plan: [h] (h < num_kv_heads) the number of flagged rows of KV head
+// h, then, from guard_list_offset, one list per KV head of
+// guard_head_segment(rows_per_head) entries, whose first [h] are the head's
+// flagged rows (head row indices: rank, Q head of the group, token) in any
+// order — a row's fixup result does not depend on the rows gathered with
+// it.  Head h's rows form ceil([h] / 128) groups of 128, numbered head by
+// head.
+__host__ __device__ __forceinline__ int guard_list_offset(int num_kv_heads) { return (num_kv_heads + 3) / 4 * 4; }
+__host__ __device__ __forceinline__ int guard_head_segment(int rows_per_head) {
+    return (rows_per_head + kRowsPerGroup - 1) / kRowsPerGroup * kRowsPerGroup;
+}
+
+// Shape of the rows a guard plan indexes.
+struct GuardShape {
+    int64_t rows_total;   // pcp * Hq * local_q
+    int32_t rows_per_head;
+    int32_t group_rows;   // group * local_q
+    int32_t local_q;
+    int32_t num_q_heads;
+    int32_t num_kv_heads;
+    int32_t group;
+    int32_t max_sparse;   // 128-row groups the sparse partials hold
+};
+
+// Flag-array index ([pcp, Hq, local_q] order) of row r of KV head `head`.
+__device__ __forceinline__ int64_t guard_row_index(const GuardShape& g, int head, int r) {
+    const int rank = r / g.group_rows;
+    const int rem = r - rank * g.group_rows;
+    const int hig = rem / g.local_q;
+    const int tok = rem - hig * g.local_q;
+    return ((int64_t)(rank * g.num_q_heads + head * g.group + hig)) * g.local_q + tok;
+}
+
+// KV head and head row index of the row at flag-array index `row`.
+__device__ __forceinline__ int guard_head_row(const GuardShape& g, int64_t row, int& head) {
+    const int64_t rh = row / g.local_q;
+    const int tok = (int)(row - rh * g.local_q);
+    const int rank = (int)(rh / g.num_q_heads);
+    const int qh = (int)(rh - (int64_t)rank * g.num_q_heads);
+    head = qh / g.group;
+    return (rank * g.group + (qh - head * g.group)) * g.local_q + tok;
+}
+
+// Groups of 128 rows in a plan.
+__device__ __forceinline__ int guard_groups(const int32_t* plan, int heads) {
+    int total = 0;
+    for (int h = 0; h < heads; ++h) total += (plan[h] + kRowsPerGroup - 1) / kRowsPerGroup;
+    return total;
+}
+
+// Group `slot` (< guard_groups) of a plan: its KV head, the list index of its
+// first row and the head's row count.
+struct GuardGroup {
+    int head;
+    int first;
+    int count;
+};
+__device__ __forceinline__ GuardGroup guard_group(const int32_t* plan, int heads, int slot) {
+    GuardGroup g{0, 0, 0};
+    int before = 0;
+    for (int h = 0; h < heads; ++h) {
+        const int count = plan[h];
+        const int n = (count + kRowsPerGroup - 1) / kRowsPerGroup;
+        if (slot >= before && slot < before + n) g = GuardGroup{h, (slot - before) * kRowsPerGroup, count};
+        before += n;
+    }
+    return g;
 }
 
 // ln(E[(1 + f) / 2^f]) for f uniform in [0, 1): how much the linear-mantissa

@@ -1,14 +1,15 @@
 // Precision guard of the e4m3-MFMA history kernels: the plan of the BF16
 // fixup and the merge of its split partials.
 //
-// The e4m3 pass writes one flag byte per query row (probability mass below
-// PCPA_GUARD_MIN_MASS).  guard_plan_kernel gathers the flagged rows of each
-// KV head into groups of 128 (the BF16 tile kernel's 4 waves x 32 rows).
-// Few groups: sparse mode, where the fixup splits each group's history walk
-// over several workgroups (bounded latency) and guard_merge_kernel combines
-// the ranges; many: dense mode, one workgroup per group, writing the output
-// directly.  With no flagged row every fixup and merge workgroup exits at
-// once.
+// The guard plan (common.hpp) lists, per KV head, the query rows whose
+// probability mass is below PCPA_GUARD_MIN_MASS.  A one-pass e4m3 launch
+// writes one flag byte per row and guard_plan_kernel lists them; a split
+// launch's merge appends the rows itself.  The fixup gathers them into groups
+// of 128 (the BF16 tile kernel's 4 waves x 32 rows).  Few groups: sparse
+// mode, where the fixup splits each group's history walk over several
+// workgroups (bounded latency) and guard_merge_kernel combines the ranges;
+// many: dense mode, one workgroup per group, writing the output directly.
+// With no flagged row every fixup and merge workgroup exits at once.
 #pragma once
 
 #include "common.hpp"
@@ -21,28 +22,6 @@ constexpr int kGuardMaxHeads = 64;
 // Capacity of the sparse partials, in query rows over all history ranges:
 // [splits, slots * 128] FP32 rows of D + 1 values (67 MB at head_dim 256).
 constexpr int64_t kGuardPartialRows = 65536;
-
-struct GuardShape {
-    int64_t rows_total;   // pcp * Hq * local_q
-    int32_t rows_per_head;
-    int32_t group_rows;   // group * local_q
-    int32_t local_q;
-    int32_t num_q_heads;
-    int32_t num_kv_heads;
-    int32_t group;
-    int32_t max_sparse;   // 128-row groups the sparse partials hold
-};
-
-
-// Flag-array index ([pcp, Hq, local_q] order) of row r of KV head `head`
-// (rows of a head in the kernels' order: rank, Q head of the group, token).
-__device__ __forceinline__ int64_t guard_row_index(const GuardShape& g, int head, int r) {
-    const int rank = r / g.group_rows;
-    const int rem = r - rank * g.group_rows;
-    const int hig = rem / g.local_q;
-    const int tok = rem - hig * g.local_q;
-    return ((int64_t)(rank * g.num_q_heads + head * g.group + hig)) * g.local_q + tok;
-}
 
 // Block-wide exclusive prefix of x over the workgroup's threads (thread
 // order), and the total.  Uses `wave_sum` (kGuardPlanThreads / 64 ints).
@@ -66,12 +45,8 @@ __device__ __forceinline__ int block_exclusive_scan(int x, int* wave_sum, int& t
     return before + incl - x;
 }
 
-// One workgroup.  Lists every flagged row, grouped by KV head: head h's rows
-// (in the kernels' order: rank, Q head of the group, token) fill its segment
-// of the list in ascending order, padded with -1 to a multiple of 128 rows.
-// plan[0] = 128-row groups, plan[1] = mode, plan[2 + h] = first group of
-// head h (h < num_kv_heads, plan[2 + num_kv_heads] = plan[0]), then the
-// list (plan + guard_list_offset) of head rows.  Deterministic.
+// One workgroup.  Writes the guard plan of the flag bytes: each KV head's
+// flagged row count and its list of head rows, in ascending order.
 __global__ void __launch_bounds__(kGuardPlanThreads) guard_plan_kernel(const uint8_t* flags, GuardShape g,
                                                                       int32_t* plan) {
     __shared__ int wave_sum[kGuardPlanThreads / 64];
@@ -79,6 +54,7 @@ __global__ void __launch_bounds__(kGuardPlanThreads) guard_plan_kernel(const uin
     __shared__ int next[kGuardMaxHeads];  // head h's next free list position
     const int tid = threadIdx.x;
     const int heads = g.num_kv_heads;
+    const int segment = guard_head_segment(g.rows_per_head);
     for (int i = tid; i < kGuardMaxHeads; i += kGuardPlanThreads) head_count[i] = 0;
     __syncthreads();
     // Rows are visited in [pcp, Hq, local_q] order, `unit` consecutive rows
@@ -101,12 +77,7 @@ __global__ void __launch_bounds__(kGuardPlanThreads) guard_plan_kernel(const uin
         } else {
             bits = flags[row] ? 1u : 0u;
         }
-        const int64_t rh = row / g.local_q;
-        const int tok = (int)(row - rh * g.local_q);
-        const int rank = (int)(rh / g.num_q_heads);
-        const int qh = (int)(rh - (int64_t)rank * g.num_q_heads);
-        head = qh / g.group;
-        head_row = (rank * g.group + (qh - head * g.group)) * g.local_q + tok;
+        head_row = guard_head_row(g, row, head);
         return bits;
     };
     // ---- count each head's flagged rows (the common case: none, done) -----
@@ -119,31 +90,14 @@ __global__ void __launch_bounds__(kGuardPlanThreads) guard_plan_kernel(const uin
             atomicAdd(&head_count[head], __builtin_popcount(bits));
         }
     }
-    if (!__syncthreads_or(any)) {
-        if (tid == 0) {
-            plan[0] = 0;
-            plan[1] = kGuardNone;
-        }
-        return;
+    const bool flagged = __syncthreads_or(any);
+    for (int h = tid; h < heads; h += kGuardPlanThreads) {
+        plan[h] = head_count[h];
+        next[h] = h * segment;
     }
+    if (!flagged) return;
     int32_t* const list = plan + guard_list_offset(heads);
-    if (tid == 0) {
-        int first = 0;
-        for (int h = 0; h < heads; ++h) {
-            plan[2 + h] = first;
-            next[h] = first * kRowsPerGroup;
-            first += (head_count[h] + kRowsPerGroup - 1) / kRowsPerGroup;
-        }
-        plan[2 + heads] = first;
-        plan[0] = first;
-        plan[1] = first <= g.max_sparse ? kGuardSparse : kGuardDense;
-    }
     __syncthreads();
-    // -1 padding of every segment's last group
-    for (int h = 0; h < heads; ++h) {
-        const int padded = (head_count[h] + kRowsPerGroup - 1) / kRowsPerGroup * kRowsPerGroup;
-        for (int i = head_count[h] + tid; i < padded; i += kGuardPlanThreads) list[next[h] + i] = -1;
-    }
     // ---- write the rows in order: kUnits consecutive units per thread -----
     constexpr int kUnits = 4;
     for (int64_t c0 = 0; c0 < units; c0 += (int64_t)kGuardPlanThreads * kUnits) {
@@ -184,7 +138,7 @@ __global__ void __launch_bounds__(kGuardPlanThreads) guard_plan_kernel(const uin
 // lse.  Thread t takes 8 consecutive d (t % d_vec8) of the ranges t /
 // d_vec8, t / d_vec8 + groups, ...; the groups' sums meet in LDS, so the
 // dependent loads per thread are splits / groups rather than splits.
-// Other modes, padding and slots past the list: nothing.
+// Dense mode, and slot rows past the listed rows: nothing.
 constexpr int kGuardMergeThreads = 256;
 
 __global__ void __launch_bounds__(kGuardMergeThreads) guard_merge_kernel(const float* part_o, const float* part_lse,
@@ -192,15 +146,15 @@ __global__ void __launch_bounds__(kGuardMergeThreads) guard_merge_kernel(const f
                                                                          int d_vec8, uint8_t* out, float* lse_out) {
     __shared__ float red[kGuardMergeThreads * 8];
     __shared__ float wred[kGuardMergeThreads];
-    if (plan[1] != kGuardSparse) return;
+    const int groups_listed = guard_groups(plan, g.num_kv_heads);
     const int64_t slot_row = blockIdx.x;
     const int slot = (int)(slot_row / kRowsPerGroup);
-    if (slot >= plan[0]) return;
-    const int r = plan[guard_list_offset(g.num_kv_heads) + slot_row];
-    if (r < 0) return;
-    int head = 0;
-    while (plan[2 + head + 1] <= slot) ++head;
-    const int64_t row = guard_row_index(g, head, r);
+    if (groups_listed > g.max_sparse || slot >= groups_listed) return;
+    const GuardGroup gg = guard_group(plan, g.num_kv_heads, slot);
+    const int idx = gg.first + (int)(slot_row - (int64_t)slot * kRowsPerGroup);
+    if (idx >= gg.count) return;
+    const int r = plan[guard_list_offset(g.num_kv_heads) + gg.head * guard_head_segment(g.rows_per_head) + idx];
+    const int64_t row = guard_row_index(g, gg.head, r);
     const int D = d_vec8 * 8;
     const int tid = threadIdx.x;
     const int groups = kGuardMergeThreads / d_vec8;  // d_vec8 divides 256 (D = 64, 128, 256)

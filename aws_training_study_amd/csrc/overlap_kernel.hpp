@@ -561,6 +561,11 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     constexpr int DMAW = kWaves / 2;
     using P = DmaPlan<D, DMAW>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * S::RING];
+    if constexpr (SPLIT) {
+        // a guarded split launch starts the guard plan's row counts at zero
+        // (its merge appends the flagged rows)
+        if (a.guard_zero && blockIdx.x == 0 && (int)threadIdx.x < a.num_kv_heads) a.guard_zero[threadIdx.x] = 0;
+    }
 
     // ---- XCD-aware work mapping (as history_fwd_kernel) ---------------------
     // Items run row tile fastest, so an XCD's workgroups share one (KV head,
@@ -757,14 +762,15 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
 // consecutive d).  out = sum_s w_s O_s / sum_s w_s with w_s = e^(lse_s - max),
 // bf16; lse (optional) = max + ln(sum_s w_s).  HBM bound: 4 * D + 4 bytes read
 // per row and split, 2 * D written.
-// Precision guard (guard_out set): the row's probability mass against the
+// Precision guard (guard_plan set): the row's probability mass against the
 // largest range reference m_ref = max_s part_m, sum_s l_s 2^(m_s - m_ref) / 2^6
 // = e^(lse + lse_bias - m_ref ln 2) (lse_bias: what the kernel subtracted
-// from its log-sum-exps), compared with min_mass.
+// from its log-sum-exps); a row below min_mass is appended to the guard
+// plan.
 __global__ void __launch_bounds__(256) merge_splits_kernel(const float* part_o, const float* part_lse, int splits,
                                                            int64_t rows, int d_vec8, uint8_t* out, float* lse_out,
-                                                           const float* part_m, uint8_t* guard_out, float lse_bias,
-                                                           float min_mass) {
+                                                           const float* part_m, int32_t* guard_plan, GuardShape g,
+                                                           float lse_bias, float min_mass) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= rows * d_vec8) return;
     const int64_t row = idx / d_vec8;
@@ -801,11 +807,18 @@ __global__ void __launch_bounds__(256) merge_splits_kernel(const float* part_o, 
     *(v4i*)(out + (row * D + d0) * 2) = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
     const float lse = wsum > 0.f ? mx + __logf(wsum) : -INFINITY;
     if (lse_out && d0 == 0) lse_out[row] = lse;
-    if (guard_out && d0 == 0) {
+    if (guard_plan && d0 == 0) {
         float m_ref = -INFINITY;
         for (int sp = 0; sp < splits; ++sp) m_ref = fmaxf(m_ref, part_m[sp * rows + row]);
         const float mass = wsum > 0.f ? __expf(lse + lse_bias - m_ref * kLn2) : 0.f;
-        guard_out[row] = mass < min_mass ? 1 : 0;
+        if (mass < min_mass) {
+            // append the row to its KV head's list (the split kernel zeroed the counts)
+            int head;
+            const int head_row = guard_head_row(g, row, head);
+            const int pos = atomicAdd(&guard_plan[head], 1);
+            guard_plan[guard_list_offset(g.num_kv_heads) + head * guard_head_segment(g.rows_per_head) + pos] =
+                head_row;
+        }
     }
 }
 

@@ -9,8 +9,9 @@
 //
 // Two attention kernels share the data layout and operand maps (common.hpp):
 //   * history_fwd_kernel<D, STORE8, FP8, CAUSAL> (tile_kernel.hpp): 4 waves x
-//     32 rows per workgroup, two workgroups per CU (one for bf16 MFMAs at
-//     head_dim 256), double-buffered tiles; every head
+//     32 rows per workgroup, two workgroups per CU (bf16 MFMAs at head_dim
+//     256: 8 waves in key-split pairs, one workgroup), double-buffered
+//     tiles; every head
 //     dim (64, 128, 256) and precision (e4m3 or bf16 MFMAs) other than e4m3
 //     at 256; with CAUSAL, the current tokens' causal step and its
 //     log-sum-exp merge.
@@ -175,7 +176,8 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
     const WorkspaceLayout w = workspace_layout(p, splits);
     if (w.bytes > 0 && (!workspace || workspace_bytes < w.bytes)) return PCPA_ERR_WORKSPACE;
     uint8_t* const ws = (uint8_t*)workspace;
-    uint8_t* const flags = guard ? ws + w.flags : nullptr;
+    uint8_t* const flags = guard && splits == 1 ? ws + w.flags : nullptr;
+    int32_t* const plan = guard ? (int32_t*)(ws + w.plan) : nullptr;
     const bool fast = !(p->flags & PCPA_FLAG_EXACT_EXP2);
 
     FwdArgs a = history_args(p, q, kv_pages, block_table, page_valid_len, out, lse);
@@ -200,6 +202,7 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
         a.part_o = (float*)(ws + w.part_o);
         a.part_lse = (float*)(ws + w.part_lse);
         a.part_m = guard ? (float*)(ws + w.part_m) : nullptr;
+        a.guard_zero = plan;
         if (overlap)
             fn = fast ? (const void*)ovl::history_fwd_overlap<256, true, false, true>
                       : (const void*)ovl::history_fwd_overlap<256, false, false, true>;
@@ -212,32 +215,34 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
     const int threads = overlap ? ovl::kThreads : tile_threads(p->head_dim, fp8);
     if (hipLaunchKernel(fn, dim3(8 * ((items + 7) / 8)), dim3(threads), args, 0, stream) != hipSuccess)
         return PCPA_ERR_LAUNCH;
+    GuardShape g{};
+    g.rows_total = (int64_t)p->pcp_size * p->num_q_heads * p->local_q_len;
+    g.rows_per_head = a.rows_per_head;
+    g.group_rows = a.group_rows;
+    g.local_q = a.local_q;
+    g.num_q_heads = a.num_q_heads;
+    g.num_kv_heads = a.num_kv_heads;
+    g.group = a.group;
+    g.max_sparse = w.guard_slots;
     if (splits > 1) {
-        const int64_t rows = (int64_t)p->pcp_size * p->num_q_heads * p->local_q_len;
+        // the merge also lists the guard's rows (the split kernel zeroed the counts)
         const int d_vec8 = p->head_dim / 8;
-        const int64_t threads = rows * d_vec8;
+        const int64_t threads = g.rows_total * d_vec8;
         hipLaunchKernelGGL(merge_splits_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
-                           (const float*)a.part_o, (const float*)a.part_lse, splits, rows, d_vec8, (uint8_t*)out, lse,
-                           (const float*)a.part_m, flags, overlap && fast ? kFastLseBias : 0.f,
+                           (const float*)a.part_o, (const float*)a.part_lse, splits, g.rows_total, d_vec8,
+                           (uint8_t*)out, lse, (const float*)a.part_m, plan, g, overlap && fast ? kFastLseBias : 0.f,
                            (float)PCPA_GUARD_MIN_MASS);
         if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
     }
     if (guard) {
         // the BF16 fixup of the flagged rows' 128-row tiles (BF16 MFMAs over
-        // the exactly widened cache): plan, fixup, merge of its ranges
-        GuardShape g;
-        g.rows_total = (int64_t)p->pcp_size * p->num_q_heads * p->local_q_len;
-        g.rows_per_head = a.rows_per_head;
-        g.group_rows = a.group_rows;
-        g.local_q = a.local_q;
-        g.num_q_heads = a.num_q_heads;
-        g.num_kv_heads = a.num_kv_heads;
-        g.group = a.group;
-        g.max_sparse = w.guard_slots;
-        int32_t* const plan = (int32_t*)(ws + w.plan);
-        hipLaunchKernelGGL(guard_plan_kernel, dim3(1), dim3(kGuardPlanThreads), 0, stream, (const uint8_t*)flags, g,
-                           plan);
-        if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
+        // the exactly widened cache): plan (one pass; a split launch's merge
+        // listed the rows), fixup, merge of its ranges
+        if (splits == 1) {
+            hipLaunchKernelGGL(guard_plan_kernel, dim3(1), dim3(kGuardPlanThreads), 0, stream,
+                               (const uint8_t*)flags, g, plan);
+            if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
+        }
         FwdArgs b = history_args(p, q, kv_pages, block_table, page_valid_len, out, lse);
         b.row_tiles = (a.rows_per_head + kRowsPerGroup - 1) / kRowsPerGroup;
         b.guard_plan = plan;

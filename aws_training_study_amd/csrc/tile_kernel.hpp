@@ -243,9 +243,12 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, uint32_t rt_off
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
     const float mxs = halves_max(mx) * cscale;
-    if (__builtin_amdgcn_ballot_w64(mxs > st.m + S::RESCALE_LOG2) != 0) {
-        const float m_new = fmaxf(st.m, mxs);
-        const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+    const bool raise = mxs > st.m + S::RESCALE_LOG2;
+    if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+        // only the rows past the margin move (alpha = 1 exactly elsewhere), so
+        // a row's result does not depend on the rows that share its wave
+        const float m_new = raise ? mxs : st.m;
+        const float alpha = raise ? __builtin_amdgcn_exp2f(st.m - m_new) : 1.f;
         st.l *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) st.o[dt] *= alpha;
@@ -440,9 +443,10 @@ __device__ __forceinline__ void tile_step(const FwdArgs& a, const TileCursor& cu
 }
 
 // Query row of lane j of the wave in 32-row slot pw: its index among the
-// KV head's rows (FIXUP: the plan's gathered row, -1 for padding), whether
-// it exists, its rank and local token, and the byte offset of its Q and
-// output rows in [pcp, Hq, local_q, D] bf16.
+// KV head's rows (FIXUP: entry fix_first + 32 pw + j of the head's list in
+// the guard plan, -1 past its fix_count rows), whether it exists, its rank
+// and local token, and the byte offset of its Q and output rows in [pcp, Hq,
+// local_q, D] bf16.
 struct QueryRow {
     int row;
     bool ok;
@@ -451,11 +455,15 @@ struct QueryRow {
     int64_t off;
 };
 template <int D, bool FIXUP>
-__device__ __forceinline__ QueryRow query_row(const FwdArgs& a, int head, int slot, int row_tile, int pw, int j) {
+__device__ __forceinline__ QueryRow query_row(const FwdArgs& a, int head, int row_tile, int pw, int j, int fix_first,
+                                              int fix_count) {
     QueryRow r;
-    if constexpr (FIXUP)
-        r.row = a.guard_plan[guard_list_offset(a.num_kv_heads) + slot * kRowsPerGroup + pw * kRowsPerWave + j];
-    else
+    if constexpr (FIXUP) {
+        const int idx = fix_first + pw * kRowsPerWave + j;
+        r.row = idx < fix_count ? a.guard_plan[guard_list_offset(a.num_kv_heads) +
+                                               head * guard_head_segment(a.rows_per_head) + idx]
+                                : -1;
+    } else
         r.row = row_tile * kRowsPerGroup + pw * kRowsPerWave + j;
     r.ok = FIXUP ? r.row >= 0 : r.row < a.rows_per_head;
     const int rowc = r.ok ? r.row : (FIXUP ? 0 : a.rows_per_head - 1);
@@ -475,12 +483,12 @@ __device__ __forceinline__ QueryRow query_row(const FwdArgs& a, int head, int sl
 // SPLIT: the workgroup walks only its split's share of the table entries
 // and writes a normalised FP32 partial output and log-sum-exp (merged by
 // merge_splits_kernel).
-// FIXUP: the BF16-MFMA pass of a precision-guarded launch.  The plan
-// (guard_plan_kernel) gathers the rows the e4m3 pass flagged into groups of
-// 128 rows of one KV head; in sparse mode workgroup b takes group b / splits
-// and walks history range b % splits into the guard partials (merged by
-// guard_merge_kernel), in dense mode it takes group b and writes the output
-// directly; workgroups past the plan exit at once.
+// FIXUP: the BF16-MFMA pass of a precision-guarded launch.  The guard plan
+// lists the rows the e4m3 pass flagged, in groups of 128 rows of one KV
+// head; in sparse mode (at most guard_slots groups) workgroup b takes group
+// b / splits and walks history range b % splits into the guard partials
+// (merged by guard_merge_kernel), in dense mode it takes group b and writes
+// the output directly; workgroups past the plan exit at once.
 template <int D, bool STORE8, bool FP8, bool CAUSAL = false, bool SPLIT = false, bool FIXUP = false>
 __global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileShape<D, STORE8, FP8>::PAIR ? 1 : 2))
     history_fwd_kernel(FwdArgs a) {
@@ -492,6 +500,11 @@ __global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileSha
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S::LDS_BYTES];
     __shared__ int wave_limit[S::WAVES];
     __shared__ float pair_ml[S::PAIR ? kWaves * 64 * 2 : 1];  // PAIR: the partners' (m, l) per lane
+    if constexpr (SPLIT) {
+        // a guarded split launch starts the guard plan's row counts at zero
+        // (its merge appends the flagged rows)
+        if (a.guard_zero && blockIdx.x == 0 && (int)threadIdx.x < a.num_kv_heads) a.guard_zero[threadIdx.x] = 0;
+    }
 
     // ---- XCD-aware work mapping ------------------------------------------
     // Workgroups are dealt to the 8 XCDs round-robin by launch index; give
@@ -505,23 +518,24 @@ __global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileSha
     // XCD's workgroups share one (KV head, split) and its pages.
     int splits = SPLIT ? a.splits : 1;
     const int items = a.row_tiles * a.num_kv_heads * splits;
-    int head, row_tile, split = 0, slot = 0;
+    int head, row_tile, split = 0, slot = 0, fix_first = 0, fix_count = 0;
     bool sparse = false;
     if constexpr (FIXUP) {
-        const int listed = a.guard_plan[0], mode = a.guard_plan[1];
-        sparse = mode == kGuardSparse;
+        const int listed = guard_groups(a.guard_plan, a.num_kv_heads);
+        sparse = listed <= a.guard_slots;
         if (sparse) {
             if ((int)blockIdx.x >= listed * a.splits) return;
             splits = a.splits;
             slot = blockIdx.x / splits;
             split = blockIdx.x - slot * splits;
         } else {
-            if (mode != kGuardDense || (int)blockIdx.x >= listed) return;
+            if ((int)blockIdx.x >= listed) return;
             slot = blockIdx.x;
         }
-        // the KV head whose segment of the plan holds this group
-        head = 0;
-        while (a.guard_plan[2 + head + 1] <= slot) ++head;
+        const GuardGroup gg = guard_group(a.guard_plan, a.num_kv_heads, slot);
+        head = gg.head;
+        fix_first = gg.first;
+        fix_count = gg.count;
         row_tile = 0;
     } else if constexpr (CAUSAL) {
         const int item = blockIdx.x;
@@ -563,7 +577,7 @@ __global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileSha
     const int gl = lane & 15;
 
     // ---- this lane's query row -------------------------------------------
-    const QueryRow qr = query_row<D, FIXUP>(a, head, slot, row_tile, pw, j);
+    const QueryRow qr = query_row<D, FIXUP>(a, head, row_tile, pw, j, fix_first, fix_count);
     const int rank = qr.rank, tok = qr.tok;
     const uint8_t* const qrow = a.q + qr.off;
 

@@ -22,10 +22,9 @@ carry the softmax) from a kernel bug.  It follows the kernels' arithmetic:
     ``2^(s c - m + 6)`` rounded to e4m3, either as the code
     ``round(8 x + 56)`` of the linear-mantissa exp2 (``exp2="fast"``) or as
     ``e4m3(2^x)`` (``"exact"``);
-  - ``tile`` (e4m3 MFMAs at head_dim 64/128): the reference starts at -inf
-    and moves to ``max(m, tile_max * c)`` for every row of a 32-row wave as
-    soon as one row's tile maximum exceeds its reference by 2.5;
-    probabilities ``e4m3(2^(s c - m + 6))``;
+  - ``tile`` (e4m3 MFMAs at head_dim 64/128): per row, the reference starts
+    at -inf and moves to ``tile_max * c`` when that exceeds it by more than
+    2.5; probabilities ``e4m3(2^(s c - m + 6))``;
 
   with the row sum ``l`` taken over the rounded probabilities and both ``l``
   and ``O`` rescaled by ``2^(m_old - m_new)``;
@@ -54,7 +53,6 @@ MAX_FLOOR = np.float32(-1.0e30)
 FAST_LSE_BIAS = 0.03987
 LOG2E = np.float32(1.4426950408889634)
 FP8_MAX = np.float32(448.0)
-WAVE_ROWS = 32
 
 
 def round_e4m3(x: np.ndarray) -> np.ndarray:
@@ -117,7 +115,7 @@ def _tiles(walk: list[tuple[int, int]]) -> list[tuple[int, int, int]]:
     return [(page, base, min(KEY_TILE, n - base)) for page, n in walk for base in range(0, n, KEY_TILE)]
 
 
-def _softmax_walk(scores, v_tiles, tiles, cscale, kernel, exp2, wave_of_row, q_round=True, p_round=True):
+def _softmax_walk(scores, v_tiles, tiles, cscale, kernel, exp2, q_round=True, p_round=True):
     """Online softmax over the tiles for rows sharing one KV head.
 
     scores: fp32 raw scores ``[R, keys]`` in walk order; v_tiles: float64
@@ -139,12 +137,7 @@ def _softmax_walk(scores, v_tiles, tiles, cscale, kernel, exp2, wave_of_row, q_r
         if kernel == "overlap":
             m_new = np.maximum(m, (mxs - np.float32(2.5)).astype(np.float32))
         else:
-            raise_ = mxs > (m + np.float32(2.5))
-            wave_any = np.zeros(rows, dtype=bool)
-            for w in np.unique(wave_of_row):
-                sel = wave_of_row == w
-                wave_any[sel] = bool(raise_[sel].any())
-            m_new = np.where(wave_any, np.maximum(m, mxs), m).astype(np.float32)
+            m_new = np.where(mxs > (m + np.float32(2.5)), mxs, m).astype(np.float32)
         with np.errstate(invalid="ignore"):
             alpha = np.exp2((m - m_new).astype(np.float32).astype(np.float64))
         alpha = np.where(np.isnan(alpha), 0.0, alpha)
@@ -177,9 +170,7 @@ def emulate_rows(q_bits, pool_codes, block_table, page_valid_len, *, num_kv_head
     ``block_table``/``page_valid_len``: int ``[pcp, max_local_blocks]``.
     ``rows``: ``None`` for every row (returns out float64 ``[pcp, Hq,
     local_q, D]`` and lse ``[pcp, Hq, local_q]``), or an int array of
-    ``(rank, q_head, token)`` triples (returns ``[n, D]`` and ``[n]``; the
-    ``tile`` kernel's rows are modelled with the whole 32-row wave they share
-    a reference max with).  ``q_round``/``p_round`` switch the two roundings
+    ``(rank, q_head, token)`` triples (returns ``[n, D]`` and ``[n]``).  ``q_round``/``p_round`` switch the two roundings
     off (the model is then plain float64 attention up to fp32 factors).
 
     ``return_mass``: also return each row's probability mass ``l / 2^6``, the
@@ -214,10 +205,7 @@ def emulate_rows(q_bits, pool_codes, block_table, page_valid_len, *, num_kv_head
         for g in range(num_kv_heads):
             sel = rows[:, 1] // group == g
             if sel.any():
-                hr = head_row(rows[sel, 0], rows[sel, 1], rows[sel, 2])
-                waves = np.unique(hr // WAVE_ROWS)
-                full = (waves[:, None] * WAVE_ROWS + np.arange(WAVE_ROWS)[None, :]).reshape(-1)
-                wanted.append((g, full[full < pcp * group * lq]))
+                wanted.append((g, np.unique(head_row(rows[sel, 0], rows[sel, 1], rows[sel, 2]))))
     results = {}
     for g, head_rows in wanted:
         allbits = q_bits[:, g * group:(g + 1) * group].reshape(-1, d)
@@ -229,7 +217,6 @@ def emulate_rows(q_bits, pool_codes, block_table, page_valid_len, *, num_kv_head
             else:
                 q8, sigma = decode_bfloat16(rbits), np.ones(rbits.shape[0], dtype=np.float32)
             cscale = (sigma * score_scale).astype(np.float32)
-            wave_of_row = idx // WAVE_ROWS
             parts = []
             for tiles in walks:
                 if not tiles:
@@ -239,7 +226,7 @@ def emulate_rows(q_bits, pool_codes, block_table, page_valid_len, *, num_kv_head
                 keys = np.concatenate([pool[p, 0, g, b:b + n] for p, b, n in tiles])
                 vals = np.concatenate([pool[p, 1, g, b:b + n] for p, b, n in tiles])
                 scores = _f32(q8 @ keys.T)
-                o, l, m = _softmax_walk(scores, vals, tiles, cscale, kernel, exp2, wave_of_row, q_round, p_round)
+                o, l, m = _softmax_walk(scores, vals, tiles, cscale, kernel, exp2, q_round, p_round)
                 with np.errstate(divide="ignore", invalid="ignore"):
                     part_out = np.where(l[:, None] > 0, o * (v_scale / l)[:, None], 0.0)
                     part_lse = np.where(l > 0, np.log(l) + (m.astype(np.float64) - P_BIAS_LOG2) * np.log(2.0) - bias,

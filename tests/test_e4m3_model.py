@@ -83,22 +83,28 @@ def test_without_rounding_it_is_float64_attention(kernel, head_dim):
 
 
 def _scalar_row(q_bits_row, keys, vals, tiles, c_factor, kernel, exp2):
-    """One row of the overlap kernel's arithmetic written as a plain loop."""
+    """One row of a kernel's arithmetic written as a plain loop: the overlap
+    kernel's reference trails the tile maximum by 2.5 from a -1e30 floor;
+    the tile kernel's starts at -inf and jumps to the tile maximum when that
+    exceeds it by more than 2.5."""
     q = orc.decode_bfloat16(q_bits_row).astype(np.float32)
     amax = np.float32(np.abs(q).max())
     inv = np.float32(448.0) / amax
     sigma = amax / np.float32(448.0)
     q8 = np.array([em.round_e4m3(np.float32(x * inv)) for x in q])
     c = np.float32(sigma * c_factor)
-    m = np.float32(-1.0e30)
+    m = np.float32(-1.0e30) if kernel == "overlap" else np.float32(-np.inf)
     o = np.zeros(vals.shape[1])
     l = 0.0
     key = 0
     for n in tiles:
         s = [np.float32(float(np.dot(q8, keys[key + i]))) for i in range(n)]
         mxs = np.float32(np.float32(max(s)) * c)
-        m_new = max(m, np.float32(mxs - np.float32(2.5)))
-        alpha = 2.0 ** float(np.float32(m - m_new))
+        if kernel == "overlap":
+            m_new = max(m, np.float32(mxs - np.float32(2.5)))
+        else:
+            m_new = mxs if mxs > np.float32(m + np.float32(2.5)) else m
+        alpha = 2.0 ** float(np.float32(m - m_new)) if m_new != m else 1.0
         m = m_new
         o *= alpha
         l *= alpha
@@ -115,11 +121,11 @@ def _scalar_row(q_bits_row, keys, vals, tiles, c_factor, kernel, exp2):
     return o / l
 
 
-@pytest.mark.parametrize("exp2", ["fast", "exact"])
-def test_vectorised_model_equals_a_scalar_loop(exp2):
-    cfg, problem = _problem(head_dim=256, actual_history_len=777, seed=9)
+@pytest.mark.parametrize("kernel,exp2", [("overlap", "fast"), ("overlap", "exact"), ("tile", "exact")])
+def test_vectorised_model_equals_a_scalar_loop(kernel, exp2):
+    cfg, problem = _problem(head_dim=256 if kernel == "overlap" else 128, actual_history_len=777, seed=9)
     rows = np.array([[0, 0, 0], [1, 3, 63], [0, 2, 17]])
-    out, _ = _model(cfg, problem, kernel="overlap", exp2=exp2, rows=rows)
+    out, _ = _model(cfg, problem, kernel=kernel, exp2=exp2, rows=rows)
     qbits, pool, table, lens = _inputs(problem)
     walk = em.walk_pages(table, lens, pool.shape[0], cfg.block_size)
     tiles = em._tiles(walk)
@@ -130,7 +136,7 @@ def test_vectorised_model_equals_a_scalar_loop(exp2):
         g = qh // group
         keys = np.concatenate([dec[p, 0, g, b:b + n] for p, b, n in tiles])
         vals = np.concatenate([dec[p, 1, g, b:b + n] for p, b, n in tiles])
-        want = _scalar_row(qbits[rank, qh, tok], keys, vals, [n for _, _, n in tiles], c_factor, "overlap", exp2)
+        want = _scalar_row(qbits[rank, qh, tok], keys, vals, [n for _, _, n in tiles], c_factor, kernel, exp2)
         np.testing.assert_allclose(out[i], want * problem.v_scale, rtol=1e-12, atol=1e-12)
 
 
