@@ -200,6 +200,8 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
     } else {
         a.splits = splits;
         a.part_o = (float*)(ws + w.part_o);
+        // fp16 partials where |O| <= 448 v_scale stays well inside fp16's range
+        a.part_f16 = overlap && fabsf(p->v_scale) * kFp8Max < 32768.f ? 1 : 0;
         a.part_lse = (float*)(ws + w.part_lse);
         a.part_m = guard ? (float*)(ws + w.part_m) : nullptr;
         a.guard_zero = plan;
@@ -229,7 +231,8 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
         const int d_vec8 = p->head_dim / 8;
         const int64_t threads = g.rows_total * d_vec8;
         hipLaunchKernelGGL(merge_splits_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
-                           (const float*)a.part_o, (const float*)a.part_lse, splits, g.rows_total, d_vec8,
+                           (const float*)a.part_o, a.part_f16, (const float*)a.part_lse, splits, g.rows_total,
+                           d_vec8,
                            (uint8_t*)out, lse, (const float*)a.part_m, plan, g, overlap && fast ? kFastLseBias : 0.f,
                            (float)PCPA_GUARD_MIN_MASS);
         if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;

@@ -165,7 +165,8 @@ int32_t pcpa_history_attention_lse(const pcpa_params* params, const void* q, con
  * precision guard.
  * Split history, for workloads with few query rows: the table entries are cut
  * into `splits` equal ranges, each (row tile, range) pair runs as its own
- * workgroup and writes a normalised FP32 partial output, log-sum-exp and
+ * workgroup and writes a normalised FP32 (e4m3 head_dim-256 path with
+ * 448 * v_scale < 32768: FP16) partial output, log-sum-exp and
  * reference maximum into `workspace`, and a second launch merges the
  * partials by log-sum-exp into `out` (and `lse`, optional).  Results equal
  * pcpa_history_attention_lse's to rounding.  For a launch whose (row tile,
