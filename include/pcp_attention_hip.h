@@ -62,12 +62,12 @@ extern "C" {
  *     W = sum_k 2^(x_k - m)        (x_k the score in log2 units, m the
  *                                    running reference, at most 2.5 below
  *                                    the row's largest x_k)
- * and a second launch recomputes, with BF16 MFMAs on the exactly widened
- * cache (bf16 Q and P), every workgroup holding a row with
- * W < PCPA_GUARD_MIN_MASS: short histories and peaked score distributions.
- * The second launch's workgroups exit at once when none of their rows is
- * flagged.  Needs a workspace of pcpa_split_workspace_bytes bytes (one byte
- * per query row for the flags), so it is accepted by
+ * and a later launch recomputes, with BF16 MFMAs on the exactly widened
+ * cache (bf16 Q and P), every row with W < PCPA_GUARD_MIN_MASS (short
+ * histories and peaked score distributions), the rows gathered 128 to a
+ * workgroup.  Its workgroups exit at once when no row is listed.  Needs a
+ * workspace of pcpa_split_workspace_bytes bytes (row flags, per-head row
+ * lists and the recomputation's partials), so it is accepted by
  * pcpa_history_attention_split only (any splits); the other entry points
  * return PCPA_ERR_WORKSPACE. */
 #define PCPA_FLAG_PRECISION_GUARD 4u
@@ -175,7 +175,7 @@ int32_t pcpa_history_attention_lse(const pcpa_params* params, const void* q, con
  * dtype, precision and head dim of pcpa_history_attention_lse; splits in
  * [1, PCPA_MAX_SPLITS] (1 = one pass).
  * With PCPA_FLAG_PRECISION_GUARD the workspace also holds the guard's row
- * flags, and the BF16 pass follows the e4m3 one (or the merge).
+ * flags and lists, and the BF16 pass follows the e4m3 one (or the merge).
  * workspace: device memory of at least pcpa_split_workspace_bytes(params,
  * splits) bytes (0 for splits = 1 without the guard, when NULL is
  * accepted), 16-byte aligned; its contents need no initialisation and are
