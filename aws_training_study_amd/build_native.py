@@ -3,7 +3,8 @@
 ``python -m aws_training_study_amd.build_native`` compiles
 ``csrc/pcp_attention_hip.hip`` (which includes the kernel headers in
 ``csrc/``) into ``_lib/libpcp_attention_hip.so``.  hipcc cross-compiles for
-gfx950 without a GPU present.
+gfx950 without a GPU present.  Then gcc builds ``csrc/abi_example.c``, a
+plain C caller of the library, into ``_lib/abi_example``.
 """
 
 from __future__ import annotations
@@ -19,6 +20,8 @@ REPO_ROOT = PACKAGE_DIR.parent
 SOURCES = [PACKAGE_DIR / "csrc" / "pcp_attention_hip.hip"]
 INCLUDE_DIR = REPO_ROOT / "include"
 OUTPUT = PACKAGE_DIR / "_lib" / "libpcp_attention_hip.so"
+EXAMPLE_SOURCE = PACKAGE_DIR / "csrc" / "abi_example.c"
+EXAMPLE = PACKAGE_DIR / "_lib" / "abi_example"
 OFFLOAD_ARCH = "gfx950"
 
 # Packed FP32 VALU forms are disabled for all device code.
@@ -52,6 +55,42 @@ def compile_command(output: Path = OUTPUT) -> list[str]:
     ]
 
 
+def example_command(output: Path = EXAMPLE) -> list[str]:
+    """gcc line of the C caller: the header, the HIP runtime's C API, the
+    library beside it (rpath $ORIGIN)."""
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    return [
+        "gcc",
+        "-O2",
+        "-std=c11",
+        "-Wall",
+        "-Werror",
+        "-D__HIP_PLATFORM_AMD__",
+        f"-I{INCLUDE_DIR}",
+        f"-I{rocm}/include",
+        os.fspath(EXAMPLE_SOURCE),
+        f"-L{OUTPUT.parent}",
+        "-lpcp_attention_hip",
+        f"-L{rocm}/lib",
+        "-lamdhip64",
+        "-Wl,-rpath,$ORIGIN",
+        f"-Wl,-rpath,{rocm}/lib",
+        "-o",
+        os.fspath(output),
+    ]
+
+
+def build_example(verbose: bool = False) -> Path:
+    """Compile the C caller against the built library."""
+    cmd = example_command()
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"gcc failed ({result.returncode}):\n{result.stderr}")
+    return EXAMPLE
+
+
 def build(verbose: bool = False) -> Path:
     """Compile the library; always recompiles. Returns the output path."""
     OUTPUT.parent.mkdir(parents=True, exist_ok=True)
@@ -67,6 +106,7 @@ def build(verbose: bool = False) -> Path:
     if verbose and stderr.strip():
         print(stderr, file=sys.stderr)
     os.replace(tmp, OUTPUT)
+    build_example(verbose)
     return OUTPUT
 
 

@@ -1,0 +1,119 @@
+"""The C ABI from a plain C program (aws_training_study_amd/csrc/abi_example.c,
+built by __graft_entry__.build() with gcc): no Python or torch between the
+caller and the library.
+
+* CPU: the program's parameter validation (pcpa_check_params on a struct it
+  read from a file) agrees with the ctypes binding, case by case.
+* GPU: it copies a problem to device memory itself, calls
+  pcpa_history_attention_lse and writes the output; that equals the Python
+  path's one-pass output and log-sum-exp bit for bit, and meets the bar
+  against the float64 oracle (max-abs 2e-2, mean-abs 2e-3).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from aws_training_study_amd import _native
+from aws_training_study_amd.build_native import EXAMPLE
+from aws_training_study_amd.pcp_attention import make_history_attention_kernel
+from aws_training_study_amd.pcp_attention.config import PCPAttentionConfig
+from aws_training_study_amd.pcp_attention.workloads import build_paged_problem, build_workload_problem
+from oracle import pcp_oracle as orc
+
+from test_gpu_parity import _assert_close, _real_history
+
+
+@pytest.fixture(scope="module")
+def example():
+    if not EXAMPLE.exists():
+        pytest.fail("abi_example is not built; run __graft_entry__.build()")
+    return EXAMPLE
+
+
+def _params(**kw):
+    p = dict(abi_version=_native.ABI_VERSION, pcp_size=4, num_q_heads=8, num_kv_heads=2, head_dim=64, local_q_len=64,
+             block_size=128, max_local_blocks=4, num_pages=16, q_dtype=1, kv_dtype=1, out_dtype=1,
+             softmax_scale=0.125, k_scale=1.0, v_scale=1.0, flags=0)
+    p.update(kw)
+    return _native.PcpaParams(**p)
+
+
+CHECK_CASES = [
+    {}, {"head_dim": 96}, {"kv_dtype": 2, "head_dim": 256}, {"num_kv_heads": 3}, {"flags": 16}, {"abi_version": 0},
+    {"pcp_size": 0}, {"block_size": 96}, {"q_dtype": 2}, {"num_pages": 0},
+]
+
+
+@pytest.mark.parametrize("case", CHECK_CASES, ids=[",".join(f"{k}={v}" for k, v in c.items()) or "valid"
+                                                   for c in CHECK_CASES])
+def test_c_caller_validates_like_the_binding(example, tmp_path, case):
+    lib = _native.load_library()
+    params = _params(**case)
+    path = tmp_path / "params.bin"
+    path.write_bytes(bytes(params))
+    res = subprocess.run([str(example), "check", str(path)], capture_output=True, text=True, timeout=60)
+    assert res.returncode == 0, res.stderr
+    want = lib.pcpa_check_params(ctypes.byref(params))
+    assert res.stdout.split()[:2] == ["status", str(want)], res.stdout
+
+
+def _write_inputs(directory, params, problem):
+    (directory / "params.bin").write_bytes(bytes(params))
+    (directory / "q.bin").write_bytes(problem.q_stacked.contiguous().view(torch.int16).numpy().tobytes())
+    kv = problem.kv_pages.contiguous()
+    kv = kv.view(torch.int16) if kv.dtype == torch.bfloat16 else kv.view(torch.uint8)
+    (directory / "kv.bin").write_bytes(kv.numpy().tobytes())
+    (directory / "table.bin").write_bytes(problem.block_table.to(torch.int32).contiguous().numpy().tobytes())
+    (directory / "lens.bin").write_bytes(problem.page_valid_len.to(torch.int32).contiguous().numpy().tobytes())
+
+
+C_CASES = [
+    ("tiny-gqa4-d64-bf16", None),
+    ("e4m3-d256", PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=4096, actual_history_len=3000,
+                                     backend="hip")),
+    ("e4m3-d128", PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=4096, actual_history_len=4096,
+                                     num_q_heads=16, num_kv_heads=4, head_dim=128, block_size=256,
+                                     backend="hip")),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,cfg", C_CASES, ids=[c[0] for c in C_CASES])
+def test_c_caller_matches_python_and_oracle(example, tmp_path, name, cfg, cuda_device):
+    if cfg is None:
+        problem = build_workload_problem(name, seed=77)
+    else:
+        problem = build_paged_problem(cfg.validate(), seed=77, kv_scale="per_tensor")
+    cfg = problem.config
+    kernel = make_history_attention_kernel(cfg)
+    num_pages = problem.kv_pages.shape[0]
+    params = kernel._params(num_pages, problem.k_scale, problem.v_scale)  # e4m3 MFMAs on e4m3 caches, fast exp2
+    _write_inputs(tmp_path, params, problem)
+    print(f"case {name}: abi_example run", flush=True)
+    res = subprocess.run([str(example), "run", str(tmp_path), "200"], capture_output=True, text=True, timeout=120)
+    print(res.stdout.strip(), flush=True)
+    assert res.returncode == 0, res.stderr + res.stdout
+    rows = cfg.pcp_size * cfg.num_q_heads * cfg.local_q_len
+    out_c = np.frombuffer((tmp_path / "out.bin").read_bytes(), dtype=np.uint16).reshape(
+        cfg.pcp_size, cfg.num_q_heads, cfg.local_q_len, cfg.head_dim)
+    lse_c = np.frombuffer((tmp_path / "lse.bin").read_bytes(), dtype=np.float32).reshape(
+        cfg.pcp_size, cfg.num_q_heads, cfg.local_q_len)
+    assert lse_c.size == rows
+
+    gpu = problem.to(cuda_device)
+    precision = "fp8" if cfg.kv_dtype == "fp8_e4m3fn" else "auto"
+    out_py, lse_py = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len,
+                            k_scale=problem.k_scale, v_scale=problem.v_scale, precision=precision, splits=1,
+                            return_lse=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(out_c, out_py.cpu().view(torch.int16).numpy().view(np.uint16)), "C and Python outputs differ"
+    assert np.array_equal(lse_c.view(np.uint32), lse_py.cpu().numpy().view(np.uint32)), "lse differs"
+    q, k, v = _real_history(problem)
+    exp = orc.expected_stacked(q, k, v, orc.OracleShape.from_config(cfg))
+    _assert_close(orc.decode_bfloat16(out_c), exp, f"C caller {name}")
