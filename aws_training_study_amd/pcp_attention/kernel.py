@@ -140,10 +140,13 @@ class HistoryAttentionKernel:
             raise ValueError(f"configuration rejected by the HIP kernel: {_native.status_string(status)}")
         self._default_valid = None
         # per-call host work kept small (a 14 us launch pair is otherwise host
-        # bound): launch parameters and split counts are cached
+        # bound): launch parameters, split counts and shapes are cached
         self._call_params = {}
         self._splits = {}
         self._ws_sizes = {}
+        self._q_shape = (cfg.pcp_size, cfg.num_q_heads, cfg.local_q_len, cfg.head_dim)
+        self._table_shape = (cfg.pcp_size, cfg.max_local_blocks)
+        self._modes = {p: (self.uses_bf16_mfma(p), self.guarded(p)) for p in PRECISIONS}
 
     def _params(self, num_pages: int, k_scale: float, v_scale: float):
         return self._native.PcpaParams(
@@ -172,7 +175,7 @@ class HistoryAttentionKernel:
         from .paging import valid_lengths_from_block_mask
 
         cfg = self.config
-        table_shape = (cfg.pcp_size, cfg.max_local_blocks)
+        table_shape = self._table_shape
         if page_valid_len is not None and block_valid_mask is not None:
             raise ValueError("pass either page_valid_len or block_valid_mask, not both")
         if page_valid_len is None and block_valid_mask is None:
@@ -180,7 +183,7 @@ class HistoryAttentionKernel:
         if page_valid_len is None:
             # a GPU mask is converted on the GPU (no host round trip)
             page_valid_len = valid_lengths_from_block_mask(block_valid_mask, cfg)
-        if tuple(page_valid_len.shape) != table_shape:
+        if page_valid_len.shape != table_shape:
             raise ValueError(f"page_valid_len must be {table_shape}, got {tuple(page_valid_len.shape)}")
         tokens = None
         if not page_valid_len.is_cuda:
@@ -221,8 +224,8 @@ class HistoryAttentionKernel:
         if not q.is_cuda:
             raise ValueError("q must be a GPU tensor")
         device = q.device
-        q_shape = (cfg.pcp_size, cfg.num_q_heads, cfg.local_q_len, cfg.head_dim)
-        if tuple(q.shape) != q_shape or q.dtype != torch.bfloat16 or not q.is_contiguous():
+        q_shape = self._q_shape
+        if q.shape != q_shape or q.dtype != torch.bfloat16 or not q.is_contiguous():
             raise ValueError(f"q must be contiguous bfloat16 {q_shape}, got {q.dtype} {tuple(q.shape)}")
         kv_dtype = _torch_kv_dtype(cfg.kv_dtype)
         if (
@@ -237,8 +240,8 @@ class HistoryAttentionKernel:
                 f"got {kv_pages.dtype} {tuple(kv_pages.shape)} on {kv_pages.device}"
             )
         num_pages = kv_pages.shape[0]
-        table_shape = (cfg.pcp_size, cfg.max_local_blocks)
-        if tuple(block_table.shape) != table_shape:
+        table_shape = self._table_shape
+        if block_table.shape != table_shape:
             raise ValueError(f"block_table must be {table_shape}, got {tuple(block_table.shape)}")
         if (block_table.dtype not in (torch.int32, torch.int64) or block_table.device != device
                 or not block_table.is_contiguous()):
@@ -247,14 +250,13 @@ class HistoryAttentionKernel:
         page_valid_len, tokens = self._resolve_lengths(device, page_valid_len, block_valid_mask)
         if out is None:
             out = torch.empty(q_shape, dtype=torch.bfloat16, device=device)
-        elif tuple(out.shape) != q_shape or out.dtype != torch.bfloat16 or not out.is_contiguous() or out.device != device:
+        elif out.shape != q_shape or out.dtype != torch.bfloat16 or not out.is_contiguous() or out.device != device:
             raise ValueError(f"out must be contiguous bfloat16 {q_shape} on {device}")
         lse = None
         if return_lse:
             lse = torch.empty(q_shape[:3], dtype=torch.float32, device=device)
-        bf16_mfma = self.uses_bf16_mfma(precision)
-        guard = self.guarded(precision)
-        key = (num_pages, float(k_scale), float(v_scale), bf16_mfma, exp2, guard, table64)
+        bf16_mfma, guard = self._modes[precision]
+        key = (num_pages, k_scale, v_scale, precision, exp2, table64)
         params = self._call_params.get(key)
         if params is None:
             params = self._params(num_pages, k_scale, v_scale)
@@ -278,39 +280,22 @@ class HistoryAttentionKernel:
                 n_split = self._splits[skey] = self.split_count(device, bf16_mfma, tokens)
         else:
             n_split = int(splits)
-        with torch.cuda.device(device):
-            stream = torch.cuda.current_stream(device).cuda_stream
-            if n_split > 1 or guard:
-                size = self.workspace_bytes(n_split, precision)
-                if workspace is None:
-                    workspace = self._workspace(size, device)
-                elif workspace.dtype != torch.uint8 or workspace.device != device or not workspace.is_contiguous():
-                    raise ValueError(f"workspace must be a contiguous uint8 tensor on {device}")
-                status = self._lib.pcpa_history_attention_split(
-                    ctypes.byref(params),
-                    n_split,
-                    q.data_ptr(),
-                    kv_pages.data_ptr(),
-                    block_table.data_ptr(),
-                    page_valid_len.data_ptr(),
-                    out.data_ptr(),
-                    None if lse is None else lse.data_ptr(),
-                    workspace.data_ptr(),
-                    workspace.numel(),
-                    stream,
-                )
-            else:
-                status = self._lib.pcpa_history_attention_lse(
-                    ctypes.byref(params),
-                    q.data_ptr(),
-                    kv_pages.data_ptr(),
-                    block_table.data_ptr(),
-                    page_valid_len.data_ptr(),
-                    out.data_ptr(),
-                    None if lse is None else lse.data_ptr(),
-                    stream,
-                )
-        self._native.check(status)
+        if n_split > 1 or guard:
+            size = self.workspace_bytes(n_split, precision)
+            if workspace is None:
+                workspace = self._workspace(size, device)
+            elif workspace.dtype != torch.uint8 or workspace.device != device or not workspace.is_contiguous():
+                raise ValueError(f"workspace must be a contiguous uint8 tensor on {device}")
+            status = _on_device(device, self._lib.pcpa_history_attention_split, params, n_split, q.data_ptr(),
+                                kv_pages.data_ptr(), block_table.data_ptr(), page_valid_len.data_ptr(),
+                                out.data_ptr(), None if lse is None else lse.data_ptr(), workspace.data_ptr(),
+                                workspace.numel())
+        else:
+            status = _on_device(device, self._lib.pcpa_history_attention_lse, params, q.data_ptr(),
+                                kv_pages.data_ptr(), block_table.data_ptr(), page_valid_len.data_ptr(),
+                                out.data_ptr(), None if lse is None else lse.data_ptr())
+        if status:
+            self._native.check(status)
         return (out, lse) if return_lse else out
 
     def graphed(self, q, kv_pages, block_table, block_valid_mask=None, *, warmup: int = 1, **kwargs):
@@ -414,6 +399,23 @@ class HistoryAttentionKernel:
             ws = torch.empty(max(size, 16), dtype=torch.uint8, device=device)
             self._split_ws = ws
         return ws
+
+
+def _on_device(device, fn, *args):
+    """``fn(*args, stream)`` with ``device`` current and its current torch
+    stream (raw handle) last: the launch is queued where torch would queue
+    work on that device.  Switches the current device only when it differs
+    (a switch and the stream object cost microseconds a small launch does not
+    take on the GPU)."""
+    import torch
+
+    index = device.index
+    raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if torch.cuda.current_device() == index:
+        stream = raw_stream(index) if raw_stream else torch.cuda.current_stream(device).cuda_stream
+        return fn(*args, stream)
+    with torch.cuda.device(device):
+        return fn(*args, torch.cuda.current_stream(device).cuda_stream)
 
 
 def make_history_attention_kernel(config: PCPAttentionConfig) -> HistoryAttentionKernel:
