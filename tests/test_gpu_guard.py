@@ -282,23 +282,25 @@ def test_tile_kernel_e4m3_matches_model(head_dim, tokens, cuda_device):
 # ---- what the guard recomputes
 
 
-def test_guard_recomputes_exactly_the_low_mass_rows(cuda_device):
+@pytest.mark.parametrize("splits", [1, 2])
+def test_guard_recomputes_exactly_the_low_mass_rows(splits, cuda_device):
     """Q x1.2 on the 8K workload: some rows fall below the guard mass.  Rows
     whose model mass is above 1.25x the threshold keep the e4m3 pass's output
-    bit for bit; rows below 0.8x get the BF16-MFMA result (to its rounding:
-    they are gathered into other waves than the BF16 kernel's)."""
+    bit for bit; rows below 0.8x get the BF16-MFMA result (to the rounding
+    of the fixup's split walk).  splits 1: the flags and the plan launch;
+    2: the split merge lists the rows."""
     cfg = FOUR
     problem = _problem(cfg, "none", 45)
     q = _scaled_q(problem, 1.2)
     gpu = problem.to(cuda_device)
     qd = q.to(cuda_device)
     kernel = make_history_attention_kernel(cfg)
-    kw = dict(page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale, v_scale=problem.v_scale, splits=1)
-    auto = kernel(qd, gpu.kv_pages, gpu.block_table, **kw).float().cpu().numpy()
-    fp8 = kernel(qd, gpu.kv_pages, gpu.block_table, precision="fp8", **kw).float().cpu().numpy()
-    bf16 = kernel(qd, gpu.kv_pages, gpu.block_table, precision="bf16", **kw).float().cpu().numpy()
+    kw = dict(page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale, v_scale=problem.v_scale)
+    auto = kernel(qd, gpu.kv_pages, gpu.block_table, splits=splits, **kw).float().cpu().numpy()
+    fp8 = kernel(qd, gpu.kv_pages, gpu.block_table, precision="fp8", splits=splits, **kw).float().cpu().numpy()
+    bf16 = kernel(qd, gpu.kv_pages, gpu.block_table, precision="bf16", splits=1, **kw).float().cpu().numpy()
     torch.cuda.synchronize()
-    _, _, mass = _model(problem, q, None, problem.page_valid_len, return_mass=True)
+    _, _, mass = _model(problem, q, None, problem.page_valid_len, splits=splits, return_mass=True)
     T = _native.GUARD_MIN_MASS
     kept, low = mass > 1.25 * T, mass < 0.8 * T
     print(f"rows kept {kept.sum()}, recomputed {low.sum()} of {mass.size}", flush=True)
@@ -308,17 +310,20 @@ def test_guard_recomputes_exactly_the_low_mass_rows(cuda_device):
     assert np.abs(auto[low] - fp8[low]).max() > 0
 
 
-def test_dense_fixup_equals_the_bf16_kernel(cuda_device):
-    """Q x4: every row is flagged, the plan goes dense (one pass per tile),
-    and the result is the BF16-MFMA kernel's, bit for bit."""
+@pytest.mark.parametrize("splits", [1, 2])
+def test_dense_fixup_equals_the_bf16_kernel(splits, cuda_device):
+    """Q x4: every row is flagged, the plan goes dense (one pass per group of
+    128 gathered rows), and the result is the one-pass BF16-MFMA kernel's,
+    bit for bit, whatever order the rows were listed in (splits 2: by device
+    atomics in the split merge)."""
     cfg = FOUR
     problem = _problem(cfg, "none", 46)
     q = _scaled_q(problem, 4).to(cuda_device)
     gpu = problem.to(cuda_device)
     kernel = make_history_attention_kernel(cfg)
-    kw = dict(page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale, v_scale=problem.v_scale, splits=1)
-    auto, lse = kernel(q, gpu.kv_pages, gpu.block_table, return_lse=True, **kw)
-    bf16, lse16 = kernel(q, gpu.kv_pages, gpu.block_table, precision="bf16", return_lse=True, **kw)
+    kw = dict(page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale, v_scale=problem.v_scale)
+    auto, lse = kernel(q, gpu.kv_pages, gpu.block_table, return_lse=True, splits=splits, **kw)
+    bf16, lse16 = kernel(q, gpu.kv_pages, gpu.block_table, precision="bf16", return_lse=True, splits=1, **kw)
     torch.cuda.synchronize()
     assert torch.equal(auto, bf16)
     assert torch.equal(lse, lse16)
