@@ -256,6 +256,11 @@ class HistoryAttentionKernel:
         if return_lse:
             lse = torch.empty(q_shape[:3], dtype=torch.float32, device=device)
         bf16_mfma, guard = self._modes[precision]
+        # scales by value (a tensor or numpy scalar is read here, not kept)
+        if type(k_scale) is not float:
+            k_scale = float(k_scale)
+        if type(v_scale) is not float:
+            v_scale = float(v_scale)
         key = (num_pages, k_scale, v_scale, precision, exp2, table64)
         params = self._call_params.get(key)
         if params is None:
