@@ -125,7 +125,7 @@ def _check_model(got, model, mass, label):
         assert diff[ok].mean() <= 2e-4 + np.abs(model[ok]).mean() * 2.0 ** -9, label
 
 
-# ---- short runtime histories in a long bucket (VERDICT: auto from runtime lengths)
+# ---- short runtime histories in a long bucket (precision chosen from the runtime lengths)
 
 
 @pytest.mark.parametrize("bucket", ["four-chip", "full"])
@@ -168,7 +168,7 @@ def test_auto_on_short_runtime_history_reference_mask(bucket, tokens, cuda_devic
                f"{bucket} runtime {tokens} mask auto")
 
 
-# ---- peaked scores (VERDICT: e4m3 away from unit-normal data)
+# ---- peaked scores (e4m3 away from unit-normal data)
 
 PEAKED = [("none", 2), ("none", 3), ("per_channel", 1), ("per_channel", 2), ("per_channel", 3)]
 
