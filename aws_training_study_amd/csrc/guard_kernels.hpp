@@ -167,7 +167,7 @@ __global__ void __launch_bounds__(kGuardMergeThreads) guard_merge_kernel(const f
     for (int sp = 0; sp < splits; ++sp) mx = fmaxf(mx, part_lse[sp * stride + slot_row]);
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float wsum = 0.f;
-#pragma unroll 2
+#pragma unroll 8
     for (int sp = sg; sp < splits; sp += groups) {
         const float l = part_lse[sp * stride + slot_row];
         const float w = l == -INFINITY ? 0.f : __expf(l - mx);
