@@ -15,7 +15,7 @@ from pathlib import Path
 LIB_DIR = Path(__file__).resolve().parent / "_lib"
 LIB_NAME = "libpcp_attention_hip.so"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 PCPA_OK = 0
 STATUS_NAMES = {
@@ -40,13 +40,17 @@ FLAG_BF16_MFMA = 1
 FLAG_EXACT_EXP2 = 2
 FLAG_PRECISION_GUARD = 4
 FLAG_TABLE_INT64 = 8
+FLAG_E4M3_UNGUARDED = 16
 # Rows whose probability mass sum_k 2^(x_k - m) is below this are recomputed
-# with BF16 MFMAs under FLAG_PRECISION_GUARD (PCPA_GUARD_MIN_MASS).
+# with BF16 MFMAs by the precision guard (PCPA_GUARD_MIN_MASS), which runs on
+# every e4m3-MFMA launch without FLAG_E4M3_UNGUARDED.
 GUARD_MIN_MASS = 384.0
 
 MAX_SPLITS = 64
 # Device scratch of pcpa_history_attention_noalloc, per GPU (bytes).
-NOALLOC_SCRATCH_BYTES = 128 << 20
+NOALLOC_SCRATCH_BYTES = 80 << 20
+# Guard scratch of pcpa_history_attention / _lse, per GPU (bytes).
+GUARD_SCRATCH_BYTES = 48 << 20
 
 # Every symbol the header declares; the CPU test suite checks they resolve.
 EXPORTED_SYMBOLS = (

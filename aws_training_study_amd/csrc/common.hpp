@@ -66,7 +66,7 @@ struct FwdArgs {
     // `splits` equal ranges, one per workgroup of a row tile; each writes its
     // normalised FP32 partial output and log-sum-exp, merged afterwards.
     int32_t splits;
-    int32_t part_f16;         // part_o holds fp16 values (the e4m3 overlap kernel, |V| small enough)
+    int32_t part_f16;         // part_o holds fp16 values of O / l before v_scale (the e4m3 overlap kernel)
     float* part_o;            // [splits, pcp * Hq * local_q, D] fp32 (or fp16)
     float* part_lse;          // [splits, pcp * Hq * local_q]
     float* part_m;            // [splits, pcp * Hq * local_q]: each range's reference max (log2)

@@ -20,8 +20,8 @@ constexpr int kGuardPlanThreads = 1024;
 // KV heads a guard plan handles (the guarded launch is refused beyond).
 constexpr int kGuardMaxHeads = 64;
 // Capacity of the sparse partials, in query rows over all history ranges:
-// [splits, slots * 128] FP32 rows of D + 1 values (67 MB at head_dim 256).
-constexpr int64_t kGuardPartialRows = 65536;
+// [splits, slots * 128] FP32 rows of D + 1 values (34 MB at head_dim 256).
+constexpr int64_t kGuardPartialRows = 32768;
 
 // Block-wide exclusive prefix of x over the workgroup's threads (thread
 // order), and the total.  Uses `wave_sum` (kGuardPlanThreads / 64 ints).

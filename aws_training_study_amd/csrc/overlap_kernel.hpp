@@ -712,36 +712,28 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     if constexpr (SPLIT) {
         if (row_ok) {
             const int64_t prow = (int64_t)split * a.rows_per_head * a.num_kv_heads + row_off / (D * 2);
-            if (a.part_f16) {
-                // fp16 partials (the host checked that |O| <= 448 v_scale fits):
-                // half the bytes for the split kernel to write and the merge to read
-                _Float16* const po = (_Float16*)a.part_o + prow * D;
+            // fp16 partials of O / l, before the v_scale factor (the merge
+            // applies it): a weighted mean of e4m3 V codes, |O / l| <= 448
+            // whatever v_scale is, so fp16 keeps its relative precision;
+            // half the bytes of fp32 for this kernel to write and the merge
+            // to read
+            const float inv_l = sm.l > 0.f ? 1.f / sm.l : 0.f;
+            _Float16* const po = (_Float16*)a.part_o + prow * D;
 #pragma unroll
-                for (int dt = 0; dt < DT; ++dt)
+            for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-                    for (int r4 = 0; r4 < 4; ++r4) {
-                        const int d = 32 * dt + 8 * r4 + 4 * h;
-                        uint32_t w[2];
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int d = 32 * dt + 8 * r4 + 4 * h;
+                    uint32_t w[2];
 #pragma unroll
-                        for (int i = 0; i < 2; ++i) {
-                            const _Float16 x0 = (_Float16)(o[dt][4 * r4 + 2 * i] * scale);
-                            const _Float16 x1 = (_Float16)(o[dt][4 * r4 + 2 * i + 1] * scale);
-                            w[i] = (uint32_t)__builtin_bit_cast(uint16_t, x0) |
-                                   ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
-                        }
-                        *(v2i*)(po + d) = v2i{(int)w[0], (int)w[1]};
+                    for (int i = 0; i < 2; ++i) {
+                        const _Float16 x0 = (_Float16)(o[dt][4 * r4 + 2 * i] * inv_l);
+                        const _Float16 x1 = (_Float16)(o[dt][4 * r4 + 2 * i + 1] * inv_l);
+                        w[i] = (uint32_t)__builtin_bit_cast(uint16_t, x0) |
+                               ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
                     }
-            } else {
-                float* const po = a.part_o + prow * D;
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                    for (int r4 = 0; r4 < 4; ++r4) {
-                        const int d = 32 * dt + 8 * r4 + 4 * h;
-                        *(v4f*)(po + d) = v4f{o[dt][4 * r4 + 0] * scale, o[dt][4 * r4 + 1] * scale,
-                                              o[dt][4 * r4 + 2] * scale, o[dt][4 * r4 + 3] * scale};
-                    }
-            }
+                    *(v2i*)(po + d) = v2i{(int)w[0], (int)w[1]};
+                }
             if (h == 0) {
                 a.part_lse[prow] = lse;
                 if (a.part_m) a.part_m[prow] = sm.m;
@@ -780,16 +772,18 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
 }  // namespace ovl
 
 // Merge of split partial outputs by log-sum-exp: one thread per (row, 8
-// consecutive d).  out = sum_s w_s O_s / sum_s w_s with w_s = e^(lse_s - max),
-// bf16; lse (optional) = max + ln(sum_s w_s).  HBM bound: 4 * D + 4 bytes
+// consecutive d).  out = part_scale * sum_s w_s O_s / sum_s w_s with w_s =
+// e^(lse_s - max), bf16 (part_scale: v_scale for the fp16 partials of the
+// e4m3 overlap kernel, which hold O / l before it; else 1); lse (optional)
+// = max + ln(sum_s w_s).  HBM bound: 4 * D + 4 bytes
 // (2 * D + 4 with fp16 partials) read per row and split, 2 * D written.
 // Precision guard (guard_plan set): the row's probability mass against the
 // largest range reference m_ref = max_s part_m, sum_s l_s 2^(m_s - m_ref) / 2^6
 // = e^(lse + lse_bias - m_ref ln 2) (lse_bias: what the kernel subtracted
 // from its log-sum-exps); a row below min_mass is appended to the guard
 // plan.
-__global__ void __launch_bounds__(256) merge_splits_kernel(const float* part_o, int part_f16, const float* part_lse,
-                                                           int splits, int64_t rows, int d_vec8, uint8_t* out,
+__global__ void __launch_bounds__(256) merge_splits_kernel(const float* part_o, int part_f16, float part_scale,
+                                                           const float* part_lse, int splits, int64_t rows, int d_vec8, uint8_t* out,
                                                            float* lse_out,
                                                            const float* part_m, int32_t* guard_plan, GuardShape g,
                                                            float lse_bias, float min_mass) {
@@ -831,7 +825,7 @@ __global__ void __launch_bounds__(256) merge_splits_kernel(const float* part_o, 
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = fmaf(w, x[i], acc[i]);
     }
-    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+    const float inv = wsum > 0.f ? part_scale / wsum : 0.f;
     uint32_t wv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

@@ -78,7 +78,17 @@ struct WorkspaceLayout {
     int32_t guard_splits, guard_slots, groups_total;
 };
 
-inline bool guarded(const pcpa_params* p) { return (p->flags & PCPA_FLAG_PRECISION_GUARD) != 0; }
+// A launch runs e4m3 MFMAs on an e4m3 cache unless PCPA_FLAG_BF16_MFMA.
+inline bool e4m3_mfma(const pcpa_params* p) {
+    return p->kv_dtype == PCPA_DTYPE_FP8_E4M3FN && !(p->flags & PCPA_FLAG_BF16_MFMA);
+}
+// The precision guard runs on every e4m3-MFMA launch but an explicitly
+// unguarded one.
+inline bool guarded(const pcpa_params* p) { return e4m3_mfma(p) && !(p->flags & PCPA_FLAG_E4M3_UNGUARDED); }
+// Split partials of the e4m3 overlap kernel (head_dim 256) are FP16 values of
+// O / l, before the v_scale factor (|O / l| <= 448, the largest e4m3 V code,
+// whatever v_scale is); the merge applies v_scale.  Other kernels: FP32.
+inline bool f16_partials(const pcpa_params* p) { return e4m3_mfma(p) && p->head_dim == 256; }
 
 inline int64_t align16(int64_t x) { return (x + 15) / 16 * 16; }
 
@@ -87,7 +97,7 @@ inline WorkspaceLayout workspace_layout(const pcpa_params* p, int splits) {
     WorkspaceLayout w{};
     if (splits > 1) {
         w.part_o = 0;
-        w.part_lse = w.part_o + (int64_t)splits * rows * p->head_dim * 4;
+        w.part_lse = align16(w.part_o + (int64_t)splits * rows * p->head_dim * (f16_partials(p) ? 2 : 4));
         w.part_m = w.part_lse + (int64_t)splits * rows * 4;
         w.bytes = w.part_m + (int64_t)splits * rows * 4;
     }
@@ -154,12 +164,28 @@ inline const void* tile_kernel_for(int head_dim, bool store8, bool fp8) {
     }
 }
 
+// Device memory of the guard scratch (see guard_scratch below), held for
+// one call: acquire() makes `stream` wait for the previous call's use of this
+// GPU's scratch; the destructor records this call's end for the next one.
+// Neither is recorded on a stream under graph capture.
+struct GuardLease {
+    void* ptr = nullptr;
+    int dev = -1;
+    bool capturing = false;
+    hipStream_t stream = nullptr;
+    int32_t acquire(hipStream_t s);
+    ~GuardLease();
+};
+
 // One history attention call: `splits` ranges of table entries (1: one
 // pass), then, for a precision-guarded launch on e4m3 MFMAs, the BF16-MFMA
-// pass over the workgroups whose rows the e4m3 pass flagged.
+// pass over the workgroups whose rows the e4m3 pass flagged.  With a lease
+// and no workspace, the workspace is the library's guard scratch, taken
+// after every argument check.
 inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, const void* kv_pages,
                               const void* block_table, const int32_t* page_valid_len, void* out, float* lse,
-                              void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+                              void* workspace, int64_t workspace_bytes, hipStream_t stream,
+                              GuardLease* lease = nullptr) {
     const int32_t st = pcpa_check_params(p);
     if (st != PCPA_OK) return st;
     if (splits < 1 || splits > PCPA_MAX_SPLITS) return PCPA_ERR_BAD_SHAPE;
@@ -169,11 +195,18 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
     if (((uintptr_t)block_table | (uintptr_t)page_valid_len | (uintptr_t)lse) & 3u) return PCPA_ERR_MISALIGNED;
     if ((p->flags & PCPA_FLAG_TABLE_INT64) && ((uintptr_t)block_table & 7u)) return PCPA_ERR_MISALIGNED;
     const bool store8 = p->kv_dtype == PCPA_DTYPE_FP8_E4M3FN;
-    const bool fp8 = store8 && !(p->flags & PCPA_FLAG_BF16_MFMA);
+    const bool fp8 = e4m3_mfma(p);
     const bool overlap = fp8 && p->head_dim == 256;
-    const bool guard = fp8 && guarded(p);
+    const bool guard = guarded(p);
     if (guard && p->num_kv_heads > kGuardMaxHeads) return PCPA_ERR_UNSUPPORTED;
     const WorkspaceLayout w = workspace_layout(p, splits);
+    if (w.bytes > 0 && !workspace && lease) {
+        if (w.bytes > PCPA_GUARD_SCRATCH_BYTES) return PCPA_ERR_SCRATCH;
+        const int32_t ls = lease->acquire(stream);
+        if (ls != PCPA_OK) return ls;
+        workspace = lease->ptr;
+        workspace_bytes = PCPA_GUARD_SCRATCH_BYTES;
+    }
     if (w.bytes > 0 && (!workspace || workspace_bytes < w.bytes)) return PCPA_ERR_WORKSPACE;
     uint8_t* const ws = (uint8_t*)workspace;
     uint8_t* const flags = guard && splits == 1 ? ws + w.flags : nullptr;
@@ -200,8 +233,7 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
     } else {
         a.splits = splits;
         a.part_o = (float*)(ws + w.part_o);
-        // fp16 partials where |O| <= 448 v_scale stays well inside fp16's range
-        a.part_f16 = overlap && fabsf(p->v_scale) * kFp8Max < 32768.f ? 1 : 0;
+        a.part_f16 = f16_partials(p) ? 1 : 0;
         a.part_lse = (float*)(ws + w.part_lse);
         a.part_m = guard ? (float*)(ws + w.part_m) : nullptr;
         a.guard_zero = plan;
@@ -231,8 +263,8 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
         const int d_vec8 = p->head_dim / 8;
         const int64_t threads = g.rows_total * d_vec8;
         hipLaunchKernelGGL(merge_splits_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
-                           (const float*)a.part_o, a.part_f16, (const float*)a.part_lse, splits, g.rows_total,
-                           d_vec8,
+                           (const float*)a.part_o, a.part_f16, a.part_f16 ? p->v_scale : 1.f,
+                           (const float*)a.part_lse, splits, g.rows_total, d_vec8,
                            (uint8_t*)out, lse, (const float*)a.part_m, plan, g, overlap && fast ? kFastLseBias : 0.f,
                            (float)PCPA_GUARD_MIN_MASS);
         if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
@@ -301,6 +333,65 @@ inline int32_t scratch_for_current_device(void** out) {
     return PCPA_OK;
 }
 
+// Guard scratch of pcpa_history_attention / _lse: the precision guard's
+// flags, row lists and partials of a call that brings no workspace.  One
+// copy per GPU, held until the process ends.  Calls are ordered through it
+// per GPU: each waits (on the GPU) for the previous call's last kernel.
+static __device__ __align__(256) uint8_t guard_scratch[PCPA_GUARD_SCRATCH_BYTES];
+
+struct GuardScratchState {
+    std::mutex mutex;     // held from acquire() to the end of the call's launches
+    void* ptr = nullptr;  // device address of guard_scratch on this GPU
+    hipEvent_t done{};    // the end of the last call that used it
+    bool recorded = false;
+};
+static GuardScratchState guard_state[kMaxDevices];
+
+int32_t GuardLease::acquire(hipStream_t s) {
+    int d = -1;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= kMaxDevices) return PCPA_ERR_LAUNCH;
+    GuardScratchState& g = guard_state[d];
+    g.mutex.lock();
+    dev = d;
+    stream = s;
+    if (!g.ptr) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(guard_scratch)) != hipSuccess || !ptr) return PCPA_ERR_LAUNCH;
+        if (hipEventCreateWithFlags(&g.done, hipEventDisableTiming) != hipSuccess) return PCPA_ERR_LAUNCH;
+        g.ptr = ptr;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess) return PCPA_ERR_LAUNCH;
+    capturing = cs != hipStreamCaptureStatusNone;
+    if (!capturing && g.recorded && hipStreamWaitEvent(s, g.done, 0) != hipSuccess) return PCPA_ERR_LAUNCH;
+    ptr = g.ptr;
+    return PCPA_OK;
+}
+
+GuardLease::~GuardLease() {
+    if (dev < 0) return;
+    GuardScratchState& g = guard_state[dev];
+    // recorded even after a failed launch: the kernels queued before it
+    // still use the scratch
+    if (ptr && !capturing && hipEventRecord(g.done, stream) == hipSuccess) g.recorded = true;
+    g.mutex.unlock();
+}
+
+// pcpa_history_attention / _lse: a guarded launch takes the guard scratch,
+// or runs every row on BF16 MFMAs (the guard's own precision) when its
+// guard buffers do not fit the scratch.
+inline int32_t history_one_pass(const pcpa_params* p, const void* q, const void* kv_pages, const void* block_table,
+                                const int32_t* page_valid_len, void* out, float* lse, hipStream_t stream) {
+    if (p && p->abi_version == PCPA_ABI_VERSION && pcpa_check_params(p) == PCPA_OK && guarded(p) &&
+        workspace_layout(p, 1).bytes > PCPA_GUARD_SCRATCH_BYTES) {
+        pcpa_params b = *p;
+        b.flags = (b.flags | PCPA_FLAG_BF16_MFMA) & ~(uint32_t)PCPA_FLAG_PRECISION_GUARD;
+        return history_launch(&b, 1, q, kv_pages, block_table, page_valid_len, out, lse, nullptr, 0, stream);
+    }
+    GuardLease lease;
+    return history_launch(p, 1, q, kv_pages, block_table, page_valid_len, out, lse, nullptr, 0, stream, &lease);
+}
+
 }  // namespace pcpa
 
 extern "C" {
@@ -320,7 +411,7 @@ const char* pcpa_status_string(int32_t status) {
         case PCPA_ERR_TOO_LARGE: return "sizes overflow the kernel's index arithmetic";
         case PCPA_ERR_BAD_SCALE: return "scales must be finite and positive";
         case PCPA_ERR_WORKSPACE: return "workspace missing or smaller than pcpa_split_workspace_bytes";
-        case PCPA_ERR_SCRATCH: return "launch needs more than the library's PCPA_NOALLOC_SCRATCH_BYTES of scratch";
+        case PCPA_ERR_SCRATCH: return "launch needs more than the library's fixed scratch";
         default: return "unknown status";
     }
 }
@@ -333,8 +424,9 @@ int32_t pcpa_check_params(const pcpa_params* p) {
         return PCPA_ERR_BAD_SHAPE;
     if (p->num_q_heads % p->num_kv_heads) return PCPA_ERR_BAD_SHAPE;
     if (p->flags & ~(uint32_t)(PCPA_FLAG_BF16_MFMA | PCPA_FLAG_EXACT_EXP2 | PCPA_FLAG_PRECISION_GUARD |
-                               PCPA_FLAG_TABLE_INT64))
+                               PCPA_FLAG_TABLE_INT64 | PCPA_FLAG_E4M3_UNGUARDED))
         return PCPA_ERR_BAD_SHAPE;
+    if ((p->flags & PCPA_FLAG_PRECISION_GUARD) && (p->flags & PCPA_FLAG_E4M3_UNGUARDED)) return PCPA_ERR_BAD_SHAPE;
     if (p->q_dtype != PCPA_DTYPE_BF16 || p->out_dtype != PCPA_DTYPE_BF16) return PCPA_ERR_BAD_DTYPE;
     if (p->kv_dtype != PCPA_DTYPE_BF16 && p->kv_dtype != PCPA_DTYPE_FP8_E4M3FN) return PCPA_ERR_BAD_DTYPE;
     if (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256) return PCPA_ERR_UNSUPPORTED;
@@ -355,8 +447,7 @@ int32_t pcpa_check_params(const pcpa_params* p) {
 int32_t pcpa_history_attention_lse(const pcpa_params* p, const void* q, const void* kv_pages,
                                    const void* block_table, const int32_t* page_valid_len, void* out,
                                    float* lse, void* stream) {
-    return pcpa::history_launch(p, 1, q, kv_pages, block_table, page_valid_len, out, lse, nullptr, 0,
-                                (hipStream_t)stream);
+    return pcpa::history_one_pass(p, q, kv_pages, block_table, page_valid_len, out, lse, (hipStream_t)stream);
 }
 
 int64_t pcpa_split_workspace_bytes(const pcpa_params* p, int32_t splits) {
@@ -391,8 +482,7 @@ int32_t pcpa_history_attention_noalloc(const pcpa_params* p, int32_t splits, con
 int32_t pcpa_history_attention(const pcpa_params* p, const void* q, const void* kv_pages,
                                const void* block_table, const int32_t* page_valid_len, void* out,
                                void* stream) {
-    return pcpa::history_launch(p, 1, q, kv_pages, block_table, page_valid_len, out, nullptr, nullptr, 0,
-                                (hipStream_t)stream);
+    return pcpa::history_one_pass(p, q, kv_pages, block_table, page_valid_len, out, nullptr, (hipStream_t)stream);
 }
 
 int32_t pcpa_current_attention(const pcpa_params* p, int32_t interleave, const void* q, const void* kv_current,

@@ -66,7 +66,11 @@ class HistoryAttentionKernel:
       ``[Hq, local_q, D]`` shards (stacked here).  ``out[r]`` is rank r's
       output; ``list(out)`` gives the per-rank list.
     * ``kv_pages``: ``[num_pages, 2 * Hkv * block_size * D]`` in the config's
-      ``kv_dtype``; row ``p`` is a ``pack_local_kv`` row.
+      ``kv_dtype``; row ``p`` is a ``pack_local_kv`` row.  Or the reference's
+      per-rank caches: a list of ``pcp`` ``[max_local_blocks, payload]``
+      tensors (``pool_from_local_caches``), with no block table; the third
+      positional argument is then the reference's ``block_valid_mask``, as in
+      the NKI kernel's ``(q_ref, local_kv_ref, block_valid_mask_ref)``.
     * ``block_table``: int ``[pcp, max_local_blocks]`` page of each cache block.
     * validity: ``page_valid_len`` (int ``[pcp, max_local_blocks]``), or the
       reference's ``block_valid_mask`` (run_poc.py:137-153, shared by all
@@ -101,9 +105,9 @@ class HistoryAttentionKernel:
       given), else from the config's ``actual_history_len``.
       Split partials and the guard's row flags go to ``workspace`` (a uint8
       GPU tensor of ``workspace_bytes(splits, precision)`` bytes) or, if
-      none is given, to a workspace the kernel object keeps: split or
-      guarded calls through one object that may overlap (other streams)
-      need their own.
+      none is given, to a workspace the kernel object keeps per (device,
+      current stream): calls on one stream run in order, calls on other
+      streams get workspaces of their own.
     * ``return_lse``: also return each row's log-sum-exp (float32
       ``[pcp, Hq, local_q]``, natural log of the sum of ``exp(score)`` over
       the valid history keys, ``-inf`` for none) - the input of a merge with
@@ -144,6 +148,8 @@ class HistoryAttentionKernel:
         self._call_params = {}
         self._splits = {}
         self._ws_sizes = {}
+        self._split_ws = {}
+        self._local_pools = {}
         self._q_shape = (cfg.pcp_size, cfg.num_q_heads, cfg.local_q_len, cfg.head_dim)
         self._table_shape = (cfg.pcp_size, cfg.max_local_blocks)
         self._modes = {p: (self.uses_bf16_mfma(p), self.guarded(p)) for p in PRECISIONS}
@@ -196,7 +202,7 @@ class HistoryAttentionKernel:
         self,
         q,
         kv_pages,
-        block_table,
+        block_table=None,
         block_valid_mask=None,
         *,
         page_valid_len=None,
@@ -224,6 +230,18 @@ class HistoryAttentionKernel:
         if not q.is_cuda:
             raise ValueError("q must be a GPU tensor")
         device = q.device
+        if isinstance(kv_pages, (list, tuple)):
+            # the reference's per-rank caches: kernel(q_list, local_kv_list, mask)
+            if block_table is not None and block_table.is_floating_point():
+                if block_valid_mask is not None:
+                    raise ValueError("pass the block-valid mask once")
+                block_table, block_valid_mask = None, block_table
+            if block_table is not None:
+                raise ValueError("a per-rank cache list brings its own block table (rank r's block b is page "
+                                 "r * max_local_blocks + b); pass a pool to use another")
+            kv_pages, block_table = self.pool_from_local_caches(kv_pages, device)
+        elif block_table is None:
+            raise ValueError("block_table is required with a page pool")
         q_shape = self._q_shape
         if q.shape != q_shape or q.dtype != torch.bfloat16 or not q.is_contiguous():
             raise ValueError(f"q must be contiguous bfloat16 {q_shape}, got {q.dtype} {tuple(q.shape)}")
@@ -271,6 +289,8 @@ class HistoryAttentionKernel:
                 params.flags |= self._native.FLAG_EXACT_EXP2
             if guard:
                 params.flags |= self._native.FLAG_PRECISION_GUARD
+            elif not bf16_mfma:
+                params.flags |= self._native.FLAG_E4M3_UNGUARDED
             if table64:
                 params.flags |= self._native.FLAG_TABLE_INT64
             if len(self._call_params) >= 64:
@@ -288,7 +308,7 @@ class HistoryAttentionKernel:
         if n_split > 1 or guard:
             size = self.workspace_bytes(n_split, precision)
             if workspace is None:
-                workspace = self._workspace(size, device)
+                workspace = self._workspace(size, device, _current_raw_stream(device))
             elif workspace.dtype != torch.uint8 or workspace.device != device or not workspace.is_contiguous():
                 raise ValueError(f"workspace must be a contiguous uint8 tensor on {device}")
             status = _on_device(device, self._lib.pcpa_history_attention_split, params, n_split, q.data_ptr(),
@@ -302,6 +322,41 @@ class HistoryAttentionKernel:
         if status:
             self._native.check(status)
         return (out, lse) if return_lse else out
+
+    def pool_from_local_caches(self, local_kv, device=None):
+        """(pool, identity block table) of the reference's per-rank caches.
+
+        ``local_kv``: one ``[max_local_blocks, 2 * Hkv * block_size * D]``
+        tensor per rank, ``pack_local_kv`` rows padded to ``max_local_blocks``
+        as run_poc.py:231-238 builds them (the NKI kernel's ``local_kv_ref``,
+        kernel.py:84-118).  The pool holds rank r's block b as page
+        ``r * max_local_blocks + b``.  It is built once and reused while the
+        same tensors come back unchanged (same storage, same torch version
+        counter: an in-place torch write to one of them builds it again;
+        writes that bypass torch are not seen).
+        """
+        import torch
+
+        cfg = self.config
+        if len(local_kv) != cfg.pcp_size:
+            raise ValueError(f"expected {cfg.pcp_size} per-rank caches, got {len(local_kv)}")
+        kv_dtype = _torch_kv_dtype(cfg.kv_dtype)
+        shape = (cfg.max_local_blocks, cfg.page_elements)
+        device = local_kv[0].device if device is None else device
+        for r, t in enumerate(local_kv):
+            if tuple(t.shape) != shape or t.dtype != kv_dtype or t.device != device or not t.is_contiguous():
+                raise ValueError(f"rank {r}'s cache must be contiguous {kv_dtype} {shape} on {device}, "
+                                 f"got {t.dtype} {tuple(t.shape)} on {t.device}")
+        key = (device, tuple((t.data_ptr(), t._version) for t in local_kv))
+        hit = self._local_pools.get(key)
+        if hit is not None:
+            return hit
+        pool = torch.cat(list(local_kv), dim=0)
+        table = torch.arange(cfg.pcp_size * cfg.max_local_blocks, dtype=torch.int32, device=device).reshape(
+            cfg.pcp_size, cfg.max_local_blocks)
+        self._local_pools.clear()  # the last set of caches only
+        self._local_pools[key] = (pool, table)
+        return pool, table
 
     def graphed(self, q, kv_pages, block_table, block_valid_mask=None, *, warmup: int = 1, **kwargs):
         """This call captured into a HIP graph (``launch.GraphedLaunch``).
@@ -317,6 +372,9 @@ class HistoryAttentionKernel:
 
         from .launch import GraphedLaunch
 
+        if isinstance(kv_pages, (list, tuple)):
+            raise ValueError("graphed() takes a page pool and block table (pool_from_local_caches builds them "
+                             "from per-rank caches; a graph replays against that pool)")
         if kwargs.get("out") is None:
             kwargs["out"] = torch.empty_like(q)
         if kwargs.get("workspace") is None:
@@ -370,12 +428,16 @@ class HistoryAttentionKernel:
 
     def workspace_bytes(self, n_split: int, precision: str = "auto") -> int:
         """Bytes of the workspace of a call with ``n_split`` splits and ``precision``."""
-        key = (int(n_split), self.guarded(precision))
+        key = (int(n_split), self.guarded(precision), self.uses_bf16_mfma(precision))
         size = self._ws_sizes.get(key)
         if size is None:
             params = self._params(self.config.num_pages, 1.0, 1.0)
             if key[1]:
                 params.flags |= self._native.FLAG_PRECISION_GUARD
+            elif key[2]:
+                params.flags |= self._native.FLAG_BF16_MFMA
+            else:
+                params.flags |= self._native.FLAG_E4M3_UNGUARDED
             size = self._lib.pcpa_split_workspace_bytes(ctypes.byref(params), key[0])
             if size < 0:
                 self._native.check(int(size))
@@ -396,14 +458,34 @@ class HistoryAttentionKernel:
             return None
         return torch.empty(size, dtype=torch.uint8, device=device)
 
-    def _workspace(self, size: int, device):
+    def _workspace(self, size: int, device, stream: int):
+        """The workspace this object keeps for calls on (``device``, ``stream``).
+
+        Calls on one stream run in order, so they can share one; calls on
+        different streams may overlap on the GPU, so each stream gets its own
+        (a guarded call's row flags, plan and fixup partials, or a split
+        call's partials, must not be rewritten by another call in flight).
+        """
         import torch
 
-        ws = getattr(self, "_split_ws", None)
-        if ws is None or ws.device != device or ws.numel() < size:
+        key = (device, stream)
+        ws = self._split_ws.get(key)
+        if ws is None or ws.numel() < size:
+            if ws is None and len(self._split_ws) >= 16:
+                self._split_ws.clear()
             ws = torch.empty(max(size, 16), dtype=torch.uint8, device=device)
-            self._split_ws = ws
+            self._split_ws[key] = ws
         return ws
+
+
+def _current_raw_stream(device) -> int:
+    """Raw handle of torch's current stream on ``device``."""
+    import torch
+
+    raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw_stream is not None:
+        return raw_stream(device.index)
+    return torch.cuda.current_stream(device).cuda_stream
 
 
 def _on_device(device, fn, *args):

@@ -4,10 +4,24 @@
  *
  * Plain C types only: device pointers are `const void*` / `void*`, the HIP
  * stream is passed as `void*` (a hipStream_t, or NULL for the null stream).
- * The library never allocates device memory and never synchronises the
- * host: every launch is asynchronous on the given stream.  Calls are
- * stateless and re-entrant (safe from several host threads on different
- * streams).  Status codes are returned, never printed.
+ * The library never synchronises the host: every launch is asynchronous on
+ * the given stream.  Status codes are returned, never printed.  Calls are
+ * safe from several host threads on different streams.
+ *
+ * Device memory: the library calls no hipMalloc.  Its code object holds two
+ * fixed `__device__` arrays, PCPA_GUARD_SCRATCH_BYTES + PCPA_NOALLOC_SCRATCH_BYTES
+ * = 128 MiB on every GPU a process launches any entry point on, held until
+ * the process ends:
+ *   - the guard scratch of pcpa_history_attention / _lse (the precision
+ *     guard's row flags, row lists and partials when the caller gives no
+ *     workspace).  The library orders the calls that use it on one GPU (an
+ *     event per GPU: a call's first kernel waits for the previous user's
+ *     last), except on a stream under graph capture, where no ordering is
+ *     recorded: a captured call must not replay while another call on that
+ *     GPU uses the guard scratch.
+ *   - the array of pcpa_history_attention_noalloc (not ordered by the
+ *     library).
+ * Every other entry point uses only the memory its caller passes.
  *
  * Reference interface replaced (Trainium2 NKI proof of concept):
  *   pcp_attention/kernel.py:32-556  make_history_attention_kernel(config)
@@ -27,7 +41,7 @@
 extern "C" {
 #endif
 
-#define PCPA_ABI_VERSION 2
+#define PCPA_ABI_VERSION 3
 
 /* Status codes. */
 #define PCPA_OK 0
@@ -46,8 +60,7 @@ extern "C" {
 /* params.flags bits. */
 /* Run both GEMMs as BF16 MFMAs even for an e4m3 cache: K/V are widened to
  * bf16 exactly while staged, Q and P stay bf16.  Half the MFMA rate, but no
- * e4m3 rounding of Q and P (which matters for short histories, where that
- * noise is not averaged over many keys).  Ignored for a bf16 cache. */
+ * e4m3 rounding of Q and P.  Ignored for a bf16 cache. */
 #define PCPA_FLAG_BF16_MFMA 1u
 /* FP8 MFMA path at head_dim 256: compute the e4m3 probabilities with
  * v_exp_f32 instead of the default linear-mantissa exp2 (which writes the
@@ -55,23 +68,31 @@ extern "C" {
  * the exponential between powers of two first).  Slower; ignored elsewhere,
  * where P always comes from v_exp_f32. */
 #define PCPA_FLAG_EXACT_EXP2 2u
-/* Precision guard for e4m3 MFMAs (ignored when the launch runs BF16 MFMAs).
+/* Precision guard of the e4m3 MFMAs: ON by default for every launch that
+ * runs e4m3 MFMAs (an e4m3 cache without PCPA_FLAG_BF16_MFMA); this bit
+ * asks for it explicitly and changes nothing else.
  * e4m3 Q and P carry ~3.6% relative rounding noise per element, which
- * averages away only when many keys share a row's softmax.  With this flag
- * the e4m3 pass also measures each row's probability mass
+ * averages away only when many keys share a row's softmax.  The e4m3 pass
+ * therefore also measures each row's probability mass
  *     W = sum_k 2^(x_k - m)        (x_k the score in log2 units, m the
  *                                    running reference, at most 2.5 below
  *                                    the row's largest x_k)
  * and a later launch recomputes, with BF16 MFMAs on the exactly widened
  * cache (bf16 Q and P), every row with W < PCPA_GUARD_MIN_MASS (short
  * histories and peaked score distributions), the rows gathered 128 to a
- * workgroup.  Its workgroups exit at once when no row is listed.  Needs a
- * workspace of pcpa_split_workspace_bytes bytes (row flags, per-head row
- * lists and the recomputation's partials), so it is accepted by
- * pcpa_history_attention_split only (any splits); the other entry points
- * return PCPA_ERR_WORKSPACE. */
+ * workgroup.  Its workgroups exit at once when no row is listed.  Its
+ * buffers (row flags, per-head row lists, the recomputation's partials)
+ * are in the caller's workspace (pcpa_history_attention_split, sized by
+ * pcpa_split_workspace_bytes), the allocation-free array
+ * (pcpa_history_attention_noalloc) or, for pcpa_history_attention / _lse,
+ * the library's guard scratch; a launch whose guard buffers exceed
+ * PCPA_GUARD_SCRATCH_BYTES runs every row on BF16 MFMAs there instead. */
 #define PCPA_FLAG_PRECISION_GUARD 4u
 #define PCPA_GUARD_MIN_MASS 384.0f
+/* e4m3 MFMAs without the precision guard (the fastest path; rows with few
+ * effective keys can miss a 2e-2 absolute error bar).  Must not be combined
+ * with PCPA_FLAG_PRECISION_GUARD. */
+#define PCPA_FLAG_E4M3_UNGUARDED 16u
 /* block_table holds int64 entries (torch's default integer type) instead of
  * int32; an entry outside [0, num_pages) is an empty page either way.  Also
  * accepted by pcpa_kv_cache_write. */
@@ -139,6 +160,10 @@ int32_t pcpa_check_params(const pcpa_params* params);
  * Replaces kernel.py:32-556 (history_attention_kernel) and
  * kernel.py:559-564 (wrap_for_native_torch).  Output is caller-allocated
  * (the reference kernel allocated it, kernel.py:124).
+ * flags = 0 on an e4m3 cache runs e4m3 MFMAs with the precision guard, its
+ * buffers in the library's guard scratch (calls on one GPU ordered by the
+ * library, see the top of this file); PCPA_FLAG_BF16_MFMA and
+ * PCPA_FLAG_E4M3_UNGUARDED launches use no scratch.
  */
 int32_t pcpa_history_attention(const pcpa_params* params, const void* q, const void* kv_pages,
                                const void* block_table, const int32_t* page_valid_len,
@@ -165,17 +190,19 @@ int32_t pcpa_history_attention_lse(const pcpa_params* params, const void* q, con
  * precision guard.
  * Split history, for workloads with few query rows: the table entries are cut
  * into `splits` equal ranges, each (row tile, range) pair runs as its own
- * workgroup and writes a normalised FP32 (e4m3 head_dim-256 path with
- * 448 * v_scale < 32768: FP16) partial output, log-sum-exp and
- * reference maximum into `workspace`, and a second launch merges the
- * partials by log-sum-exp into `out` (and `lse`, optional).  Results equal
+ * workgroup and writes a normalised partial output (FP32; the e4m3
+ * head_dim-256 path: FP16 before the v_scale factor, which the merge
+ * applies), log-sum-exp and reference maximum into `workspace`, and a
+ * second launch merges the partials by log-sum-exp into `out` (and `lse`,
+ * optional).  Results equal
  * pcpa_history_attention_lse's to rounding.  For a launch whose (row tile,
  * KV head) workgroups would leave CUs idle (256 rows and a CU per workgroup
  * for e4m3 MFMAs at head_dim 256, else 128 rows, two per CU).  Every cache
  * dtype, precision and head dim of pcpa_history_attention_lse; splits in
  * [1, PCPA_MAX_SPLITS] (1 = one pass).
- * With PCPA_FLAG_PRECISION_GUARD the workspace also holds the guard's row
- * flags and lists, and the BF16 pass follows the e4m3 one (or the merge).
+ * On e4m3 MFMAs (unless PCPA_FLAG_E4M3_UNGUARDED) the workspace also holds
+ * the precision guard's row flags and lists, and the BF16 pass follows the
+ * e4m3 one (or the merge).
  * workspace: device memory of at least pcpa_split_workspace_bytes(params,
  * splits) bytes (0 for splits = 1 without the guard, when NULL is
  * accepted), 16-byte aligned; its contents need no initialisation and are
@@ -201,10 +228,12 @@ int32_t pcpa_history_attention_split(const pcpa_params* params, int32_t splits, 
  * PCPA_ERR_SCRATCH.  The array needs no initialisation and keeps the last
  * call's contents; every call on one GPU shares it, so calls that overlap
  * on one GPU (several streams or host threads) race and must be ordered by
- * the caller.  No counterpart in the reference (its kernel allocates its
- * output in device memory, kernel.py:124).
+ * the caller.  No counterpart in the reference; for callers that cannot
+ * allocate.
  */
-#define PCPA_NOALLOC_SCRATCH_BYTES (128ll << 20)
+#define PCPA_NOALLOC_SCRATCH_BYTES (80ll << 20)
+/* The guard scratch of pcpa_history_attention / _lse, per GPU. */
+#define PCPA_GUARD_SCRATCH_BYTES (48ll << 20)
 int32_t pcpa_history_attention_noalloc(const pcpa_params* params, int32_t splits, const void* q,
                                        const void* kv_pages, const void* block_table,
                                        const int32_t* page_valid_len, void* out, float* lse, void* stream);

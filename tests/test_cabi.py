@@ -77,7 +77,10 @@ def _good_params(**kw):
         ({"flags": 4}, 0),
         ({"flags": 8}, 0),
         ({"flags": 15}, 0),
-        ({"flags": 16}, -3),
+        ({"flags": 16}, 0),
+        ({"flags": 27}, 0),
+        ({"flags": 20}, -3),   # the guard asked for and refused at once
+        ({"flags": 32}, -3),
         ({"q_dtype": 2}, -4),
         ({"kv_dtype": 9}, -4),
         ({"head_dim": 96}, -5),
@@ -118,8 +121,13 @@ def test_split_workspace_size_from_python():
                              backend="hip")
     kernel = make_history_attention_kernel(cfg)
     rows = cfg.pcp_size * cfg.num_q_heads * cfg.local_q_len
-    # FP32 partial output, log-sum-exp and reference max per row and split
-    assert kernel.split_workspace_bytes(3) == 3 * rows * (cfg.head_dim + 2) * 4
+    # e4m3 MFMAs at head_dim 256: fp16 partial output, fp32 log-sum-exp and
+    # reference max per row and split
+    assert kernel.split_workspace_bytes(3) == 3 * rows * (cfg.head_dim * 2 + 8)
+    bf16 = make_history_attention_kernel(PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=2048,
+                                                            actual_history_len=2048, backend="hip",
+                                                            kv_dtype="bfloat16"))
+    assert bf16.split_workspace_bytes(3) == 3 * rows * (cfg.head_dim + 2) * 4
     assert kernel.workspace_bytes(1, precision="fp8") == 0
     # the precision guard needs its flags, plan and fixup partials even for one pass
     guard = kernel.workspace_bytes(1, precision="auto")
@@ -192,9 +200,11 @@ def test_auto_split_counts(workload, bf16_mfma, expected):
 
 def test_split_entry_validates_without_a_gpu(lib):
     """pcpa_split_workspace_bytes / pcpa_history_attention_split errors come back before any HIP call."""
-    p = _good_params(kv_dtype=2, head_dim=256)  # 4 ranks x 8 heads x 64 tokens = 2048 rows
+    # unguarded e4m3 MFMAs, 4 ranks x 8 heads x 64 tokens = 2048 rows: fp16
+    # partials of O / l, fp32 log-sum-exp and reference max per row and split
+    p = _good_params(kv_dtype=2, head_dim=256, flags=16)
     size = lib.pcpa_split_workspace_bytes(ctypes.byref(p), 3)
-    assert size == 3 * 2048 * (256 + 2) * 4
+    assert size == 3 * 2048 * (256 * 2 + 8)
     assert lib.pcpa_split_workspace_bytes(ctypes.byref(p), 1) == 0
     assert lib.pcpa_split_workspace_bytes(ctypes.byref(p), 0) == -3
     assert lib.pcpa_split_workspace_bytes(ctypes.byref(p), 65) == -3
@@ -210,11 +220,19 @@ def test_split_entry_validates_without_a_gpu(lib):
         need = lib.pcpa_split_workspace_bytes(ctypes.byref(other), 4)
         assert need == 4 * 2048 * (other.head_dim + 2) * 4
         assert f(ctypes.byref(other), 4, 16, 16, 16, 16, 16, None, 16, need - 16, None) == -10
-    # the guard: no workspace through the entry points that take none
-    g = _good_params(kv_dtype=2, head_dim=256, flags=4)
-    assert lib.pcpa_split_workspace_bytes(ctypes.byref(g), 1) > 0
-    assert lib.pcpa_history_attention(ctypes.byref(g), 16, 16, 16, 16, 16, None) == -10
-    assert f(ctypes.byref(g), 1, 16, 16, 16, 16, 16, None, None, 0, None) == -10
+    # the guard (the default on an e4m3 cache, or asked for): it needs its
+    # workspace through the split entry; the one-pass entries take none (the
+    # library's guard scratch) and check every argument before using it
+    for g in (_good_params(kv_dtype=2, head_dim=256), _good_params(kv_dtype=2, head_dim=256, flags=4)):
+        assert lib.pcpa_split_workspace_bytes(ctypes.byref(g), 1) > 0
+        assert f(ctypes.byref(g), 1, 16, 16, 16, 16, 16, None, None, 0, None) == -10
+        assert lib.pcpa_history_attention(ctypes.byref(g), 16, 16, 16, 16, 0, None) == -1
+        assert lib.pcpa_history_attention(ctypes.byref(g), 8, 16, 16, 16, 16, None) == -6
+        assert lib.pcpa_history_attention_lse(ctypes.byref(g), 16, 16, 16, 16, 16, 2, None) == -6
+    # the guard's buffers of a launch beyond the guard scratch: that launch
+    # runs BF16 MFMAs instead, so its one-pass size is what matters
+    big = _good_params(kv_dtype=2, head_dim=256, pcp_size=2048, local_q_len=256)
+    assert lib.pcpa_split_workspace_bytes(ctypes.byref(big), 1) > _native.GUARD_SCRATCH_BYTES
     # an int64 block table must be 8-byte aligned
     t = _good_params(flags=8)
     assert lib.pcpa_history_attention(ctypes.byref(t), 16, 16, 20, 16, 16, None) == -6

@@ -12,6 +12,16 @@
   every MFMA result allocated until it is read (an empty asm tie), and this
   scan of the assembly checks that no read lands in a pending destination
   (the failure once gave NaN outputs).
+* m0 belongs to the LDS-DMA helpers alone.  Their inline asm writes m0 (the
+  LDS destination of global_load_lds_dwordx4) and lists it as clobbered; the
+  compiler treats m0 as reserved and does not save a value of its own across
+  the asm (it warns).  That is only safe while no code the compiler
+  generates uses m0: in every kernel, each instruction naming m0 must be the
+  helper's `s_mov_b32 m0, s<n>` directly followed by `s_nop 0` and the
+  `global_load_lds_dwordx4` it feeds, every LDS-DMA must be preceded by that
+  pair, and no instruction that reads m0 implicitly (LDS-DMA of another
+  form, relative moves, messages, GWS / append / consume, LDS-direct or
+  parameter loads) may appear.
 """
 
 from __future__ import annotations
@@ -152,3 +162,58 @@ def test_the_scan_finds_a_planted_hazard():
             "v_add_f32_e32 v50, v16, v17",
             "ds_read_b64_tr_b8 v[20:21], v40 offset:0"]
     assert not _pending_destination_reads(safe)
+
+
+# Instructions that read m0 without naming it (gfx9 ISA): LDS-DMA loads,
+# relative register moves, messages, GWS / append / consume, LDS-direct and
+# interpolation loads.
+_IMPLICIT_M0 = re.compile(r"^(buffer_load\S*\s.*\blds\b|global_load_lds\S*|s_movrel\S*|v_movrel\S*|s_sendmsg\S*|"
+                          r"ds_gws\S*|ds_append|ds_consume|ds_read_addtid\S*|ds_write_addtid\S*|"
+                          r"v_interp\S*|lds_direct\S*|lds_param\S*)")
+
+
+def _m0_misuse(lines):
+    """Instructions that break the m0 rule above, with the reason."""
+    code = [l.strip() for l in lines if l.strip() and not l.strip().startswith((";", "."))]
+    found = []
+    helper_loads = set()
+    for i, line in enumerate(code):
+        names_m0 = re.search(r"\bm0\b", line) is not None
+        if names_m0:
+            if not re.fullmatch(r"s_mov_b32 m0, s\d+", line):
+                found.append(("m0 named outside the helper", line))
+                continue
+            if code[i + 1:i + 2] != ["s_nop 0"] or not code[i + 2].startswith("global_load_lds_dwordx4"):
+                found.append(("m0 write not followed by s_nop 0 and its LDS-DMA", line))
+                continue
+            helper_loads.add(i + 2)
+    for i, line in enumerate(code):
+        if _IMPLICIT_M0.match(line) and i not in helper_loads:
+            found.append(("implicit m0 reader outside the helper", line))
+    return found
+
+
+def test_m0_is_written_and_read_only_by_the_lds_dma_helpers(device_code):
+    _, bodies = device_code
+    dma = 0
+    for name, lines in bodies.items():
+        hits = _m0_misuse(lines)
+        assert not hits, f"{name}: {hits[:3]}"
+        dma += sum(1 for l in lines if l.strip().startswith("global_load_lds_dwordx4"))
+    assert dma > 0  # the kernels do use the helpers
+
+
+def test_the_m0_scan_finds_planted_misuse():
+    good = ["s_mov_b32 m0, s12", "s_nop 0", "global_load_lds_dwordx4 v3, s[4:5] offset:1024"]
+    assert not _m0_misuse(good)
+    assert not _m0_misuse(good + ["buffer_load_dword v1, off, s[0:3], 0"])  # no lds: no m0
+    # a compiler-made m0 value, an LDS-DMA without the helper's write, a
+    # relative move and an append that read m0 implicitly
+    for planted in (["s_mov_b32 m0, -1"] + good,
+                    good + ["s_add_u32 m0, s1, 0x400"],
+                    good + ["global_load_lds_dwordx4 v3, s[4:5] offset:2048"],
+                    good + ["s_movrels_b32 s0, s8"],
+                    good + ["ds_append v1 offset:4"],
+                    good + ["buffer_load_dword v1, off, s[0:3], 0 lds"],
+                    ["s_mov_b32 m0, s12", "v_add_f32_e32 v1, v2, v3", "global_load_lds_dwordx4 v3, s[4:5]"]):
+        assert _m0_misuse(planted), planted

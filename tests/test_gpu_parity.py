@@ -246,6 +246,29 @@ def test_per_rank_list_input(cuda_device):
         kernel(shards[:-1], gpu.kv_pages, gpu.block_table)
 
 
+@pytest.mark.parametrize("name", ["tiny-gqa4-d64-bf16", "four-chip-fp8"])
+def test_per_rank_local_caches_equal_the_pool_form(name, cuda_device):
+    """The NKI kernel's per-rank call form, kernel(q_ref, local_kv_ref,
+    block_valid_mask_ref) with every rank's [max_local_blocks, payload]
+    cache (kernel.py:84-118, run_poc.py:231-238), gives the pool form's
+    output bit for bit: same pages in the same walk order, the pool here
+    shuffled by a random block table."""
+    problem = build_workload_problem(name, seed=10)
+    cfg = problem.config
+    gpu = problem.to(cuda_device)
+    kernel = make_history_attention_kernel(cfg)
+    kw = dict(k_scale=problem.k_scale, v_scale=problem.v_scale)
+    pooled = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len, **kw)
+    local_kv = [gpu.kv_pages.index_select(0, gpu.block_table[r].long()).contiguous() for r in range(cfg.pcp_size)]
+    q_list = [gpu.q_stacked[r] for r in range(cfg.pcp_size)]
+    mask = make_block_valid_mask(cfg).to(cuda_device)
+    print(f"case {name}: per-rank caches, reference mask", flush=True)
+    listed = kernel(q_list, local_kv, mask, **kw)
+    again = kernel(q_list, local_kv, mask, **kw)  # the pool built once is reused
+    torch.cuda.synchronize()
+    assert torch.equal(listed, pooled) and torch.equal(again, pooled)
+
+
 @pytest.mark.parametrize(
     "kv_dtype,head_dim,precision,splits",
     [

@@ -14,7 +14,9 @@ a probability mass of 64 or more, on the rest within one e4m3 code step of
 one key (a score on a rounding tie, summed in another order by the MFMA:
 random case 99 has such a key at an exact tie, and flipping its code in the
 model leaves 9.6e-4), and in the mean; which shows the miss is the method's
-rounding and nothing else.
+rounding and nothing else.  Such a miss may only happen below 4096 history
+tokens, and a case without a row of mass 64 must meet the bar under the
+guard instead.
 """
 
 from __future__ import annotations
@@ -117,7 +119,20 @@ def test_random_configuration(i, cuda_device):
     print(f"  e4m3 case outside the bar: vs e4m3 model on {rows_ok.mean():.2f} of the rows max={diff.max(initial=0):.3e} "
           f"excess={excess_row.max(initial=0):.3e}, rows over 5e-3: {(excess_row > 5e-3).sum()} of "
           f"{excess_row.size}", flush=True)
-    if diff.size:
-        assert (excess_row > 5e-3).mean() <= 0.01
-        assert (excess_row <= 5e-3 + flip).all()
-        assert diff.mean() <= 2e-4 + np.abs(model[ok]).mean() * 2.0 ** -9
+    # over long histories the e4m3 rounding averages away: a miss there is not
+    # the method's
+    assert cfg.actual_history_len < 4096, "e4m3 path outside the bar on a long history"
+    if not rows_ok.any():
+        # no row to hold against the model: the guarded call on the same
+        # inputs must meet the bar instead
+        auto = kernel(gpu.q_stacked, gpu.kv_pages, gpu.block_table, page_valid_len=gpu.page_valid_len,
+                      k_scale=problem.k_scale, v_scale=problem.v_scale,
+                      **{k: v for k, v in kw.items() if k != "precision"})
+        torch.cuda.synchronize()
+        a_max, a_mean = orc.max_abs_and_mean_abs(auto.float().cpu().numpy(), exp)
+        print(f"  no row of mass >= 64; guarded: max_abs={a_max:.3e} mean_abs={a_mean:.3e}", flush=True)
+        assert a_max <= MAX_ABS_TOL and a_mean <= MEAN_ABS_TOL
+        return
+    assert (excess_row > 5e-3).mean() <= 0.01
+    assert (excess_row <= 5e-3 + flip).all()
+    assert diff.mean() <= 2e-4 + np.abs(model[ok]).mean() * 2.0 ** -9

@@ -55,9 +55,11 @@ def _both(problem, flags, splits, device):
 
 
 def test_noalloc_equals_the_workspace_entry_point_on_a_large_then_a_smaller_launch(cuda_device):
-    # 1) 16 ranks, 8192-token e4m3 history, 2 history splits (68 MB of partials)
+    # 1) 16 ranks, 8192-token e4m3 history, 2 history splits, flags 0 (e4m3
+    # MFMAs with the precision guard): 34 MB of fp16 partials and 34 MB of
+    # the guard's fixup partials
     big = build_workload_problem("four-chip-fp8", seed=61)
-    print("case four-chip-fp8, e4m3 MFMAs, 2 splits", flush=True)
+    print("case four-chip-fp8, e4m3 MFMAs with the guard, 2 splits", flush=True)
     (ref_out, ref_lse), (out, lse) = _both(big, 0, 2, cuda_device)
     assert torch.equal(out, ref_out) and torch.equal(lse, ref_lse)
     assert not torch.isnan(out.float()).any()
