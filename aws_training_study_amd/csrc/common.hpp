@@ -70,14 +70,18 @@ struct FwdArgs {
     float* part_o;            // [splits, pcp * Hq * local_q, D] fp32 (or fp16)
     float* part_lse;          // [splits, pcp * Hq * local_q]
     float* part_m;            // [splits, pcp * Hq * local_q]: each range's reference max (log2)
-    // Precision guard of the e4m3-MFMA kernels.  guard_out (one byte per
-    // row, [pcp, Hq, local_q]): the one-pass e4m3 kernel writes 1 for a row
-    // whose probability mass sum_k 2^(x_k - m) is below guard_min_mass, else
-    // 0.  A split launch instead sets the row counts of the guard plan
-    // guard_zero to 0 (workgroup 0), and its merge appends the rows.
-    uint8_t* guard_out;
-    float guard_min_mass;
+    // Precision guard of the e4m3-MFMA kernels.  guard_mass (one float per
+    // row, [pcp, Hq, local_q]): the one-pass e4m3 kernel writes each row's
+    // probability mass sum_k 2^(x_k - m); the guard plan lists the rows below
+    // their KV head's threshold (guard_vstats_kernel).  A split launch
+    // instead sets the row counts of the guard plan guard_zero to 0
+    // (workgroup 0), and its merge appends the rows.  Either way workgroup 0
+    // also zeroes the vstats_words 64-bit words of the V statistics at
+    // vstats_zero, which guard_vstats_kernel accumulates next.
+    float* guard_mass;
     int32_t* guard_zero;
+    uint64_t* vstats_zero;
+    int32_t vstats_words;
     // The BF16 fixup of a guarded launch (history_fwd_kernel<..., FIXUP>):
     // the guard plan (below) and the partials' capacity in 128-row groups
     // (part_o / part_lse hold [splits, guard_slots * 128] rows): with at
@@ -112,6 +116,14 @@ struct GuardShape {
     int32_t group;
     int32_t max_sparse;   // 128-row groups the sparse partials hold
 };
+
+// Workgroup 0 of a guarded e4m3 launch: the guard plan's row counts (split
+// launches, whose merge appends the rows) and the V statistics start at
+// zero.  The kernels that read them run after this launch.
+__device__ __forceinline__ void guard_zero_counts(const FwdArgs& a) {
+    if (a.guard_zero && (int)threadIdx.x < a.num_kv_heads) a.guard_zero[threadIdx.x] = 0;
+    for (int i = threadIdx.x; i < a.vstats_words; i += blockDim.x) a.vstats_zero[i] = 0;
+}
 
 // Flag-array index ([pcp, Hq, local_q] order) of row r of KV head `head`.
 __device__ __forceinline__ int64_t guard_row_index(const GuardShape& g, int head, int r) {

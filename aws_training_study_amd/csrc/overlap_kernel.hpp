@@ -561,11 +561,7 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     constexpr int DMAW = kWaves / 2;
     using P = DmaPlan<D, DMAW>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * S::RING];
-    if constexpr (SPLIT) {
-        // a guarded split launch starts the guard plan's row counts at zero
-        // (its merge appends the flagged rows)
-        if (a.guard_zero && blockIdx.x == 0 && (int)threadIdx.x < a.num_kv_heads) a.guard_zero[threadIdx.x] = 0;
-    }
+    if (blockIdx.x == 0) guard_zero_counts(a);
 
     // ---- XCD-aware work mapping (as history_fwd_kernel) ---------------------
     // Items run row tile fastest, so an XCD's workgroups share one (KV head,
@@ -742,11 +738,11 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
         return;
     }
     if constexpr (LSE) {
-        // the log-sum-exp and/or the precision guard's flag: l / 2^6 is the
-        // row's probability mass sum_k 2^(x_k - m)
+        // the log-sum-exp and/or the precision guard's row mass: l / 2^6 is
+        // the row's probability mass sum_k 2^(x_k - m)
         if (row_ok && h == 0) {
             if (a.lse) a.lse[row_off / (D * 2)] = lse;
-            if (a.guard_out) a.guard_out[row_off / (D * 2)] = sm.l < a.guard_min_mass * 64.f ? 1 : 0;
+            if (a.guard_mass) a.guard_mass[row_off / (D * 2)] = sm.l * (1.f / 64.f);
         }
     }
     if (row_ok) {
@@ -780,13 +776,13 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
 // Precision guard (guard_plan set): the row's probability mass against the
 // largest range reference m_ref = max_s part_m, sum_s l_s 2^(m_s - m_ref) / 2^6
 // = e^(lse + lse_bias - m_ref ln 2) (lse_bias: what the kernel subtracted
-// from its log-sum-exps); a row below min_mass is appended to the guard
-// plan.
+// from its log-sum-exps); a row below its KV head's threshold guard_thr
+// (guard_vstats_kernel) is appended to the guard plan.
 __global__ void __launch_bounds__(256) merge_splits_kernel(const float* part_o, int part_f16, float part_scale,
                                                            const float* part_lse, int splits, int64_t rows, int d_vec8, uint8_t* out,
                                                            float* lse_out,
                                                            const float* part_m, int32_t* guard_plan, GuardShape g,
-                                                           float lse_bias, float min_mass) {
+                                                           float lse_bias, const float* guard_thr) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= rows * d_vec8) return;
     const int64_t row = idx / d_vec8;
@@ -839,10 +835,10 @@ __global__ void __launch_bounds__(256) merge_splits_kernel(const float* part_o, 
         float m_ref = -INFINITY;
         for (int sp = 0; sp < splits; ++sp) m_ref = fmaxf(m_ref, part_m[sp * rows + row]);
         const float mass = wsum > 0.f ? __expf(lse + lse_bias - m_ref * kLn2) : 0.f;
-        if (mass < min_mass) {
+        int head;
+        const int head_row = guard_head_row(g, row, head);
+        if (mass < guard_thr[head]) {
             // append the row to its KV head's list (the split kernel zeroed the counts)
-            int head;
-            const int head_row = guard_head_row(g, row, head);
             const int pos = atomicAdd(&guard_plan[head], 1);
             guard_plan[guard_list_offset(g.num_kv_heads) + head * guard_head_segment(g.rows_per_head) + pos] =
                 head_row;

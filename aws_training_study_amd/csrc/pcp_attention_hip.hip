@@ -70,11 +70,12 @@ inline FwdArgs common_args(const pcpa_params* p, const void* q, void* out) {
     return a;
 }
 
-// Workspace of a history launch: split partials (FP32 outputs, log-sum-exps
-// and reference maxima of every range) and, for the precision guard, the
-// row flags, the fixup plan and the fixup's split partials.
+// Workspace of a history launch: split partials (outputs, log-sum-exps and
+// reference maxima of every range) and, for the precision guard, the V
+// statistics and per-head thresholds, the row masses (one pass), the fixup
+// plan and the fixup's split partials.
 struct WorkspaceLayout {
-    int64_t part_o, part_lse, part_m, flags, plan, gpart_o, gpart_lse, bytes;
+    int64_t part_o, part_lse, part_m, vstats, thr, mass, plan, gpart_o, gpart_lse, bytes;
     int32_t guard_splits, guard_slots, groups_total;
 };
 
@@ -115,8 +116,10 @@ inline WorkspaceLayout workspace_layout(const pcpa_params* p, int splits) {
         w.guard_splits = (int32_t)gs;
         const int64_t slots = kGuardPartialRows / kRowsPerGroup / gs;
         w.guard_slots = (int32_t)(slots < w.groups_total ? slots : w.groups_total);
-        w.flags = align16(w.bytes);
-        w.plan = align16(w.flags + rows);
+        w.vstats = align16(w.bytes);
+        w.thr = w.vstats + (int64_t)vstats_words(p->num_kv_heads, p->head_dim) * 8;
+        w.mass = align16(w.thr + (int64_t)p->num_kv_heads * 4);
+        w.plan = align16(w.mass + (splits == 1 ? rows * 4 : 0));
         w.gpart_o = align16(w.plan + ((int64_t)guard_list_offset(p->num_kv_heads) +
                                       (int64_t)w.groups_total * kRowsPerGroup) * 4);
         const int64_t prow = (int64_t)w.guard_splits * w.guard_slots * kRowsPerGroup;
@@ -209,20 +212,24 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
     }
     if (w.bytes > 0 && (!workspace || workspace_bytes < w.bytes)) return PCPA_ERR_WORKSPACE;
     uint8_t* const ws = (uint8_t*)workspace;
-    uint8_t* const flags = guard && splits == 1 ? ws + w.flags : nullptr;
+    float* const mass = guard && splits == 1 ? (float*)(ws + w.mass) : nullptr;
     int32_t* const plan = guard ? (int32_t*)(ws + w.plan) : nullptr;
+    float* const thr = guard ? (float*)(ws + w.thr) : nullptr;
     const bool fast = !(p->flags & PCPA_FLAG_EXACT_EXP2);
 
     FwdArgs a = history_args(p, q, kv_pages, block_table, page_valid_len, out, lse);
     const int rows_per_group = overlap ? ovl::kRowsPerGroup : kRowsPerGroup;
     a.row_tiles = (a.rows_per_head + rows_per_group - 1) / rows_per_group;
     const void* fn = nullptr;
+    if (guard) {
+        a.vstats_zero = (uint64_t*)(ws + w.vstats);
+        a.vstats_words = vstats_words(p->num_kv_heads, p->head_dim);
+    }
     if (splits == 1) {
-        a.guard_out = flags;
-        a.guard_min_mass = PCPA_GUARD_MIN_MASS;
+        a.guard_mass = mass;
         if (overlap) {
-            // the log-sum-exp instantiation also writes the guard's flags
-            const bool aux = lse || flags;
+            // the log-sum-exp instantiation also writes the guard's row masses
+            const bool aux = lse || mass;
             fn = fast ? (aux ? (const void*)ovl::history_fwd_overlap<256, true, true>
                              : (const void*)ovl::history_fwd_overlap<256, true, false>)
                       : (aux ? (const void*)ovl::history_fwd_overlap<256, false, true>
@@ -258,6 +265,31 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
     g.num_kv_heads = a.num_kv_heads;
     g.group = a.group;
     g.max_sparse = w.guard_slots;
+    if (guard) {
+        // the V statistics of the walk and each KV head's mass threshold
+        VStatsArgs v{};
+        v.kv = a.kv;
+        v.block_table = a.block_table;
+        v.page_valid_len = a.page_valid_len;
+        v.page_stride = a.page_stride;
+        v.head_stride = a.head_stride;
+        v.num_entries = a.num_entries;
+        v.table_shift = a.table_shift;
+        v.num_pages = a.num_pages;
+        v.block_size = a.block_size;
+        v.num_kv_heads = a.num_kv_heads;
+        v.stats = (uint64_t*)(ws + w.vstats);
+        v.thr = thr;
+        v.scale = PCPA_GUARD_MIN_MASS * p->v_scale * p->v_scale / 262144.f;
+        const int slots = a.num_entries < kVStatsSlots ? a.num_entries : kVStatsSlots;
+        const void* vfn = p->head_dim == 64    ? (const void*)guard_vstats_kernel<64>
+                          : p->head_dim == 128 ? (const void*)guard_vstats_kernel<128>
+                                               : (const void*)guard_vstats_kernel<256>;
+        void* vargs[] = {&v};
+        if (hipLaunchKernel(vfn, dim3(slots * p->num_kv_heads), dim3(kVStatsThreads), vargs, 0, stream) !=
+            hipSuccess)
+            return PCPA_ERR_LAUNCH;
+    }
     if (splits > 1) {
         // the merge also lists the guard's rows (the split kernel zeroed the counts)
         const int d_vec8 = p->head_dim / 8;
@@ -266,7 +298,7 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
                            (const float*)a.part_o, a.part_f16, a.part_f16 ? p->v_scale : 1.f,
                            (const float*)a.part_lse, splits, g.rows_total, d_vec8,
                            (uint8_t*)out, lse, (const float*)a.part_m, plan, g, overlap && fast ? kFastLseBias : 0.f,
-                           (float)PCPA_GUARD_MIN_MASS);
+                           (const float*)thr);
         if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
     }
     if (guard) {
@@ -275,7 +307,7 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
         // listed the rows), fixup, merge of its ranges
         if (splits == 1) {
             hipLaunchKernelGGL(guard_plan_kernel, dim3(1), dim3(kGuardPlanThreads), 0, stream,
-                               (const uint8_t*)flags, g, plan);
+                               (const float*)mass, (const float*)thr, g, plan);
             if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
         }
         FwdArgs b = history_args(p, q, kv_pages, block_table, page_valid_len, out, lse);

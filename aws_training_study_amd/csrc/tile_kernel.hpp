@@ -500,11 +500,7 @@ __global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileSha
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S::LDS_BYTES];
     __shared__ int wave_limit[S::WAVES];
     __shared__ float pair_ml[S::PAIR ? kWaves * 64 * 2 : 1];  // PAIR: the partners' (m, l) per lane
-    if constexpr (SPLIT) {
-        // a guarded split launch starts the guard plan's row counts at zero
-        // (its merge appends the flagged rows)
-        if (a.guard_zero && blockIdx.x == 0 && (int)threadIdx.x < a.num_kv_heads) a.guard_zero[threadIdx.x] = 0;
-    }
+    if (!FIXUP && !CAUSAL && blockIdx.x == 0) guard_zero_counts(a);
 
     // ---- XCD-aware work mapping ------------------------------------------
     // Workgroups are dealt to the 8 XCDs round-robin by launch index; give
@@ -810,8 +806,7 @@ __global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileSha
     }
     // Precision guard (e4m3 MFMAs): l / 2^6 is the row's probability mass
     // sum_k 2^(x_k - m) against the running reference.
-    if (FP8 && a.guard_out && row_ok && h == 0)
-        a.guard_out[row_index] = st.l < a.guard_min_mass * 64.f ? 1 : 0;
+    if (FP8 && a.guard_mass && row_ok && h == 0) a.guard_mass[row_index] = st.l * (1.f / 64.f);
     float hist_weight = 0.f;
     if (CAUSAL && a.merge_o) {
         // out = (e^lse_h O_h + e^lse O) / (e^lse_h + e^lse)

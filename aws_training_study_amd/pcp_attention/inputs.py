@@ -103,12 +103,12 @@ def _quantize_per_tensor(x: torch.Tensor) -> tuple[torch.Tensor, float]:
     return (values / scale).to(torch.float8_e4m3fn), scale
 
 
-def make_raw_inputs(cfg: PCPAttentionConfig, seed: int, *, k_prescale: str = "none"):
+def make_raw_inputs(cfg: PCPAttentionConfig, seed: int, *, k_prescale: str = "none", v_factor: float = 1.0):
     """BF16 ``q [Hq, Q, D]``, ``k``/``v`` ``[Hkv, L, D]`` before any FP8 quantisation.
 
     Same draws as ``make_scaled_inputs`` (and, without a pre-scale, as
     ``make_inputs``) up to the storage cast; this is what a KV-cache producer
-    quantises.
+    quantises.  ``v_factor`` multiplies V (V ~ N(0, v_factor^2)).
     """
     if k_prescale not in K_PRESCALE_MODES:
         raise ValueError(f"k_prescale must be one of {K_PRESCALE_MODES}, got {k_prescale!r}")
@@ -123,6 +123,8 @@ def make_raw_inputs(cfg: PCPAttentionConfig, seed: int, *, k_prescale: str = "no
         channel = torch.Generator().manual_seed(seed + 2)
         factor = torch.rand(cfg.num_kv_heads, 1, cfg.head_dim, generator=channel) * 1.5 + 0.5
         k = (k.float() * factor).to(torch.bfloat16)
+    if v_factor != 1.0:
+        v = (v.float() * v_factor).to(torch.bfloat16)
     return q, k, v
 
 
@@ -137,10 +139,11 @@ def make_scaled_inputs(
     *,
     kv_scale: str = "none",
     k_prescale: str = "none",
+    v_factor: float = 1.0,
 ) -> HistoryInputs:
     if kv_scale not in KV_SCALE_MODES:
         raise ValueError(f"kv_scale must be one of {KV_SCALE_MODES}, got {kv_scale!r}")
-    q, k, v = make_raw_inputs(cfg, seed, k_prescale=k_prescale)
+    q, k, v = make_raw_inputs(cfg, seed, k_prescale=k_prescale, v_factor=v_factor)
     k_scale = v_scale = 1.0
     if cfg.kv_dtype == "fp8_e4m3fn":
         if kv_scale == "per_tensor":

@@ -19,6 +19,11 @@ Workloads (sizes are global; "ranks" are logical PCP ranks on one GPU):
 ``gqa8-d128-bf16``      16 ranks, 64 Q / 8 KV heads, D 128, 2048 current and
     32768 history tokens, 256-token blocks, BF16 KV, K with a per-channel
     factor in [0.5, 2].
+``full-bf16``           ``full-fp8`` with a BF16 cache (the reference's BF16-KV
+    run of the full shape, README.md:191-199).
+``four-chip-q4k-fp8``, ``four-chip-q8k-fp8``, ``four-chip-q16k-fp8``
+    ``four-chip-fp8`` with 4096, 8192 and 16384 current tokens (the
+    reference's Q sweep at an 8192-token history, README.md:156-165).
 """
 
 from __future__ import annotations
@@ -81,6 +86,19 @@ WORKLOADS: dict[str, Workload] = {
         kv_scale="per_tensor",
         random_history_len=True,
     ),
+    "full-bf16": Workload(
+        "full-bf16",
+        _hip(pcp_size=64, current_len=4096, max_history_len=131072, actual_history_len=131072,
+             kv_dtype="bfloat16"),
+    ),
+    **{
+        f"four-chip-q{q // 1024}k-fp8": Workload(
+            f"four-chip-q{q // 1024}k-fp8",
+            _hip(pcp_size=16, current_len=q, max_history_len=8192, actual_history_len=8192),
+            kv_scale="per_tensor",
+        )
+        for q in (4096, 8192, 16384)
+    },
     "gqa8-d128-bf16": Workload(
         "gqa8-d128-bf16",
         _hip(
@@ -137,9 +155,10 @@ def build_paged_problem(
     kv_scale: str = "none",
     k_prescale: str = "none",
     shuffle_pages: bool = True,
+    v_factor: float = 1.0,
 ) -> PagedProblem:
     """Generate inputs, shard them by striped ownership and page them."""
-    inputs = make_scaled_inputs(config, seed, kv_scale=kv_scale, k_prescale=k_prescale)
+    inputs = make_scaled_inputs(config, seed, kv_scale=kv_scale, k_prescale=k_prescale, v_factor=v_factor)
     if config.is_history_aligned:
         k_shards, v_shards = shard_history(inputs.k, inputs.v, config)
     else:

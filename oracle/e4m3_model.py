@@ -160,6 +160,38 @@ def _softmax_walk(scores, v_tiles, tiles, cscale, kernel, exp2, q_round=True, p_
     return o, l, m
 
 
+GUARD_MIN_MASS = 384.0
+VSTATS_KEYS = 16384
+
+
+def guard_thresholds(pool_codes, block_table, page_valid_len, *, num_kv_heads, block_size, head_dim, v_scale=1.0):
+    """The precision guard's probability-mass threshold per KV head.
+
+    ``GUARD_MIN_MASS * v_scale^2 * max_d Var(V[h, :, d])``: the population
+    variance per channel of the e4m3 V codes of head h over the keys the
+    walk visits, sampled as the kernels' statistics do (every s-th key of
+    each page's valid prefix, s the smallest power of two with valid keys /
+    s <= VSTATS_KEYS).  A row whose mass ``sum_k 2^(x_k - m)`` is below it is
+    recomputed with BF16 MFMAs.  The rounding error of e4m3 Q and P in a row
+    grows as the spread of the V values it averages over sqrt(mass), so the
+    threshold grows with the variance; 384 is where unit-variance V keeps
+    the e4m3 rows within about half the 2e-2 bar.
+    """
+    pool = E4M3FN_DECODE[np.asarray(pool_codes, dtype=np.uint8)].reshape(-1, 2, num_kv_heads, block_size, head_dim)
+    walk = walk_pages(block_table, page_valid_len, pool.shape[0], block_size)
+    total = sum(n for _, n in walk)
+    stride = 1
+    while total // stride > VSTATS_KEYS:
+        stride *= 2
+    thr = np.zeros(num_kv_heads)
+    for h in range(num_kv_heads):
+        if not walk:
+            continue
+        vals = np.concatenate([pool[page, 1, h, 0:n:stride] for page, n in walk])
+        thr[h] = GUARD_MIN_MASS * v_scale ** 2 * vals.var(axis=0).max()
+    return thr
+
+
 def emulate_rows(q_bits, pool_codes, block_table, page_valid_len, *, num_kv_heads, block_size, softmax_scale,
                  k_scale=1.0, v_scale=1.0, kernel="overlap", exp2="fast", splits=1, rows=None, q_round=True,
                  p_round=True, chunk_rows=256, return_mass=False):

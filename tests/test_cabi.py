@@ -129,10 +129,11 @@ def test_split_workspace_size_from_python():
                                                             kv_dtype="bfloat16"))
     assert bf16.split_workspace_bytes(3) == 3 * rows * (cfg.head_dim + 2) * 4
     assert kernel.workspace_bytes(1, precision="fp8") == 0
-    # the precision guard needs its flags, plan and fixup partials even for one pass
+    # the precision guard needs its row masses, plan and fixup partials even
+    # for one pass (a split call's merge takes the masses from the partials)
     guard = kernel.workspace_bytes(1, precision="auto")
-    assert guard >= rows + 4 * (4 + rows // 128)
-    assert kernel.workspace_bytes(3, precision="auto") >= kernel.split_workspace_bytes(3) + guard
+    assert guard >= 4 * rows + 4 * (4 + rows // 128)
+    assert kernel.workspace_bytes(3, precision="auto") >= kernel.split_workspace_bytes(3) + guard - 4 * rows
     with pytest.raises(_native.PcpaError, match="BAD_SHAPE"):
         kernel.split_workspace_bytes(_native.MAX_SPLITS + 1)
 

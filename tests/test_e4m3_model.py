@@ -199,3 +199,100 @@ def test_mass_is_the_probability_sum_against_the_reference():
     _, _, mass3 = _model(cfg, problem, kernel="overlap", exp2="exact", rows=rows, return_mass=True, splits=3)
     np.testing.assert_allclose(mass3, mass, rtol=0.3)  # the same keys, rounded against other references
     assert shape.head_dim == 256 and np.all(np.isfinite(lse_plain))
+
+
+# ---- the guard's threshold and the spread of V
+
+
+def _pool_with_v(cfg, v_codes_fn):
+    """A zero pool of cfg's shape whose V codes come from v_codes_fn(page, head) -> [block, D] float (e4m3 values)."""
+    pages = cfg.pcp_size * cfg.max_local_blocks
+    pool = np.zeros((pages, 2, cfg.num_kv_heads, cfg.block_size, cfg.head_dim), dtype=np.float32)
+    for page in range(pages):
+        for h in range(cfg.num_kv_heads):
+            pool[page, 1, h] = v_codes_fn(page, h)
+    codes = torch.from_numpy(pool).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    table = np.arange(pages, dtype=np.int32).reshape(cfg.pcp_size, cfg.max_local_blocks)
+    lens = np.full(table.shape, cfg.block_size, dtype=np.int32)
+    return codes.reshape(pages, -1), table, lens
+
+
+def test_guard_threshold_closed_forms():
+    """Identical V rows have no spread: threshold 0.  V codes +a_d / -a_d on
+    alternate keys have variance a_d^2 in channel d: 384 v_scale^2 max_d
+    a_d^2.  The threshold scales with v_scale^2 and ignores a common offset."""
+    cfg = PCPAttentionConfig(pcp_size=2, current_len=128, max_history_len=1024, actual_history_len=1024,
+                             block_size=128, interleave_size=32, num_q_heads=4, num_kv_heads=2, head_dim=64,
+                             backend="hip").validate()
+    kw = dict(num_kv_heads=2, block_size=128, head_dim=64)
+    row = np.linspace(-3, 3, 64).astype(np.float32)
+    same = _pool_with_v(cfg, lambda page, h: np.broadcast_to(row, (128, 64)))
+    np.testing.assert_array_equal(em.guard_thresholds(*same, v_scale=0.7, **kw), [0.0, 0.0])
+    amp = np.array([0.5, 2.0])  # head 0: channels at +-0.5 .. , head 1: up to +-2 in channel 63
+    sign = np.where(np.arange(128) % 2 == 0, 1.0, -1.0)[:, None]
+
+    def two_point(page, h):
+        a_d = np.full(64, 0.25, dtype=np.float32)
+        a_d[63] = amp[h]
+        return (sign * a_d).astype(np.float32)
+    pool = _pool_with_v(cfg, two_point)
+    np.testing.assert_allclose(em.guard_thresholds(*pool, v_scale=1.0, **kw), 384 * amp ** 2, rtol=1e-12)
+    np.testing.assert_allclose(em.guard_thresholds(*pool, v_scale=0.5, **kw), 384 * 0.25 * amp ** 2, rtol=1e-12)
+    shifted = _pool_with_v(cfg, lambda page, h: two_point(page, h) + 3.0)
+    np.testing.assert_allclose(em.guard_thresholds(*shifted, v_scale=1.0, **kw), 384 * amp ** 2, rtol=1e-12)
+
+
+def test_guard_threshold_samples_every_s_th_key_of_long_walks():
+    """Beyond 16384 valid keys the statistics take every s-th key of each
+    page (s a power of two): keys off the stride do not count."""
+    cfg = PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=32768, actual_history_len=32768,
+                             block_size=512, interleave_size=64, num_q_heads=4, num_kv_heads=1, head_dim=64,
+                             backend="hip").validate()
+    keys = np.arange(512)[:, None]
+    # on the stride (2: 32768 keys / 2 = 16384) alternate +-1; off it 448
+    v = np.where(keys % 2 == 0, np.where((keys // 2) % 2 == 0, 1.0, -1.0), 448.0)
+    pool = _pool_with_v(cfg, lambda page, h: np.broadcast_to(v, (512, 64)).astype(np.float32))
+    kw = dict(num_kv_heads=1, block_size=512, head_dim=64)
+    np.testing.assert_allclose(em.guard_thresholds(*pool, v_scale=1.0, **kw), [384.0], rtol=1e-12)
+    # half the history: 16384 keys, all of them
+    lens = pool[2].copy()
+    lens[:, cfg.max_local_blocks // 2:] = 0
+    full = em.guard_thresholds(pool[0], pool[1], lens, v_scale=1.0, **kw)
+    assert full[0] > 384 * 1e4
+
+
+def test_guard_threshold_keeps_wide_v_rows_within_half_the_bar():
+    """The e4m3 rounding error of a row grows with the spread of V.  With V ~
+    N(0, 16) over 2048 keys the rows a fixed mass threshold of 384 would
+    keep on e4m3 MFMAs reach 2e-2; the threshold 384 * v_scale^2 * max_d
+    Var(V) keeps rows within about half the bar whatever the spread (V ~
+    N(0, 1) and N(0, 16) over 2048 keys, N(0, 4) over 8192 keys, where most
+    rows are kept), as unit-variance V does at 384.  Error: the model
+    against itself with both roundings off."""
+    rng = np.random.default_rng(5)
+    rows = np.stack([rng.integers(0, 4, 64), rng.integers(0, 8, 64), rng.integers(0, 64, 64)], axis=1)
+
+    def case(tokens, v_factor):
+        cfg = PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=tokens, actual_history_len=tokens,
+                                 block_size=256, interleave_size=64, num_q_heads=8, num_kv_heads=2, head_dim=256,
+                                 backend="hip").validate()
+        problem = build_paged_problem(cfg, 7, kv_scale="per_tensor", v_factor=v_factor)
+        qbits, pool, table, lens = _inputs(problem)
+        kw = dict(num_kv_heads=2, block_size=256, softmax_scale=cfg.softmax_scale, k_scale=problem.k_scale,
+                  v_scale=problem.v_scale, rows=rows)
+        got, _, mass = em.emulate_rows(qbits, pool, table, lens, return_mass=True, **kw)
+        exact, _ = em.emulate_rows(qbits, pool, table, lens, q_round=False, p_round=False, **kw)
+        thr = em.guard_thresholds(pool, table, lens, num_kv_heads=2, block_size=256, head_dim=256,
+                                  v_scale=problem.v_scale)[rows[:, 1] // 4]
+        return np.abs(got - exact).max(axis=1), mass, thr
+
+    err, mass, thr = case(2048, 1.0)
+    assert 350 < thr.max() < 450 and (mass >= thr).sum() >= 8
+    assert err[mass >= thr].max() <= 1.2e-2
+    err, mass, thr = case(2048, 4.0)
+    assert 14 * 384 < thr.min() < 19 * 384
+    assert err[mass >= 384].max() > 2e-2          # what the fixed threshold would keep
+    assert err[mass >= thr].max(initial=0.0) <= 1.2e-2
+    err, mass, thr = case(8192, 2.0)
+    assert (mass >= thr).sum() >= 32
+    assert err[mass >= thr].max() <= 1.2e-2

@@ -118,7 +118,7 @@ def test_small_workloads_every_row(name, cuda_device):
     _assert_close(out, orc.expected_stacked(q, k, v, shape), name)
 
 
-@pytest.mark.parametrize("name", ["gqa8-d128-bf16", "full-fp8", "full-fp8-varlen"])
+@pytest.mark.parametrize("name", ["gqa8-d128-bf16", "full-fp8", "full-fp8-varlen", "full-bf16", "four-chip-q16k-fp8"])
 def test_large_workloads(name, cuda_device):
     problem = build_workload_problem(name, seed=1234)
     print(f"case {name}: {problem.config}", flush=True)
