@@ -75,13 +75,10 @@ struct FwdArgs {
     // probability mass sum_k 2^(x_k - m); the guard plan lists the rows below
     // their KV head's threshold (guard_vstats_kernel).  A split launch
     // instead sets the row counts of the guard plan guard_zero to 0
-    // (workgroup 0), and its merge appends the rows.  Either way workgroup 0
-    // also zeroes the vstats_words 64-bit words of the V statistics at
-    // vstats_zero, which guard_vstats_kernel accumulates next.
+    // (workgroup 0), and its merge appends the rows; a one-pass launch's
+    // guard_list_kernel does the same after it.
     float* guard_mass;
     int32_t* guard_zero;
-    uint64_t* vstats_zero;
-    int32_t vstats_words;
     // The BF16 fixup of a guarded launch (history_fwd_kernel<..., FIXUP>):
     // the guard plan (below) and the partials' capacity in 128-row groups
     // (part_o / part_lse hold [splits, guard_slots * 128] rows): with at
@@ -117,12 +114,11 @@ struct GuardShape {
     int32_t max_sparse;   // 128-row groups the sparse partials hold
 };
 
-// Workgroup 0 of a guarded e4m3 launch: the guard plan's row counts (split
-// launches, whose merge appends the rows) and the V statistics start at
-// zero.  The kernels that read them run after this launch.
+// Workgroup 0 of a guarded e4m3 launch: the guard plan's row counts start
+// at zero (the merge of a split launch, or guard_list_kernel after a
+// one-pass launch, appends the rows).
 __device__ __forceinline__ void guard_zero_counts(const FwdArgs& a) {
     if (a.guard_zero && (int)threadIdx.x < a.num_kv_heads) a.guard_zero[threadIdx.x] = 0;
-    for (int i = threadIdx.x; i < a.vstats_words; i += blockDim.x) a.vstats_zero[i] = 0;
 }
 
 // Flag-array index ([pcp, Hq, local_q] order) of row r of KV head `head`.

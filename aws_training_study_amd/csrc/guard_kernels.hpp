@@ -13,8 +13,9 @@
 // of standard deviation 4.  guard_vstats_kernel measures it after the e4m3
 // pass.  The guard plan (common.hpp) lists, per KV head, the query rows
 // whose mass is below it: a one-pass e4m3 launch writes each row's mass and
-// guard_plan_kernel lists them; a split launch's merge appends the rows
-// itself.  The fixup gathers them into groups
+// guard_list_kernel lists them; a split launch's merge appends the rows
+// itself (either way by device atomics, in an order that depends on
+// timing, which a row's fixup result does not).  The fixup gathers them into groups
 // of 128 (the BF16 tile kernel's 4 waves x 32 rows).  Few groups: sparse
 // mode, where the fixup splits each group's history walk over several
 // workgroups (bounded latency) and guard_merge_kernel combines the ranges;
@@ -26,123 +27,43 @@
 
 namespace pcpa {
 
-constexpr int kGuardPlanThreads = 1024;
 // KV heads a guard plan handles (the guarded launch is refused beyond).
 constexpr int kGuardMaxHeads = 64;
 // Capacity of the sparse partials, in query rows over all history ranges:
 // [splits, slots * 128] FP32 rows of D + 1 values (34 MB at head_dim 256).
 constexpr int64_t kGuardPartialRows = 32768;
 
-// Block-wide exclusive prefix of x over the workgroup's threads (thread
-// order), and the total.  Uses `wave_sum` (kGuardPlanThreads / 64 ints).
-__device__ __forceinline__ int block_exclusive_scan(int x, int* wave_sum, int& total) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int incl = x;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(incl, off);
-        if (lane >= off) incl += y;
-    }
-    if (lane == 63) wave_sum[wave] = incl;
-    __syncthreads();
-    int before = 0;
-    total = 0;
-    for (int w = 0; w < kGuardPlanThreads / 64; ++w) {
-        before += w < wave ? wave_sum[w] : 0;
-        total += wave_sum[w];
-    }
-    __syncthreads();  // wave_sum is rewritten by the next scan
-    return before + incl - x;
-}
+// Rows per thread and threads per workgroup of guard_list_kernel.
+constexpr int kGuardListRows = 4;
+constexpr int kGuardListThreads = 256;
 
-// One workgroup.  Writes the guard plan of the row masses: each KV head's
-// count of rows below its threshold and its list of head rows, in ascending
-// order.
-__global__ void __launch_bounds__(kGuardPlanThreads) guard_plan_kernel(const float* mass, const float* thr,
+// The guard plan of a one-pass launch: every row whose mass (written by the
+// e4m3 pass) is below its KV head's threshold is appended to the head's
+// list with a device atomic (the e4m3 pass zeroed the counts), as the split
+// merge does.  The list order depends on timing, which the fixup's result
+// does not.  Grid: ceil(rows / (kGuardListRows * kGuardListThreads)).
+__global__ void __launch_bounds__(kGuardListThreads) guard_list_kernel(const float* mass, const float* thr,
                                                                       GuardShape g, int32_t* plan) {
-    __shared__ int wave_sum[kGuardPlanThreads / 64];
-    __shared__ int head_count[kGuardMaxHeads];
-    __shared__ int next[kGuardMaxHeads];  // head h's next free list position
-    const int tid = threadIdx.x;
-    const int heads = g.num_kv_heads;
+    const int64_t row0 = ((int64_t)blockIdx.x * kGuardListThreads + threadIdx.x) * kGuardListRows;
+    if (row0 >= g.rows_total) return;
+    float m[kGuardListRows];
+    if (row0 + kGuardListRows <= g.rows_total) {
+        const v4f x = *(const v4f*)(mass + row0);
+#pragma unroll
+        for (int i = 0; i < kGuardListRows; ++i) m[i] = x[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < kGuardListRows; ++i) m[i] = row0 + i < g.rows_total ? mass[row0 + i] : INFINITY;
+    }
+    int32_t* const list = plan + guard_list_offset(g.num_kv_heads);
     const int segment = guard_head_segment(g.rows_per_head);
-    for (int i = tid; i < kGuardMaxHeads; i += kGuardPlanThreads) head_count[i] = 0;
-    __syncthreads();
-    // Rows are visited in [pcp, Hq, local_q] order, `unit` consecutive rows
-    // at a time (16 when local_q is a multiple of 16: four 16-byte loads, one
-    // Q head; else 1); restricted to KV head h that is head h's row order.
-    const bool chunked = (g.local_q & 15) == 0;
-    const int unit = chunked ? 16 : 1;
-    const int64_t units = g.rows_total / unit;
-    // rows of unit u below their head's threshold, one bit each, and the
-    // unit's KV head and head row
-    auto load_unit = [&](int64_t u, int& head, int& head_row) -> uint32_t {
-        const int64_t row = u * unit;
-        head_row = guard_head_row(g, row, head);
-        const float t = thr[head];
-        uint32_t bits = 0;
-        if (chunked) {
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const v4f x = *(const v4f*)(mass + row + 4 * w);
-#pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    if (x[b] < t) bits |= 1u << (4 * w + b);
-            }
-        } else {
-            bits = mass[row] < t ? 1u : 0u;
-        }
-        return bits;
-    };
-    // ---- count each head's flagged rows (the common case: none, done) -----
-    int any = 0;
-    for (int64_t u = tid; u < units; u += kGuardPlanThreads) {
-        int head, head_row;
-        const uint32_t bits = load_unit(u, head, head_row);
-        if (bits) {
-            any = 1;
-            atomicAdd(&head_count[head], __builtin_popcount(bits));
-        }
-    }
-    const bool flagged = __syncthreads_or(any);
-    for (int h = tid; h < heads; h += kGuardPlanThreads) {
-        plan[h] = head_count[h];
-        next[h] = h * segment;
-    }
-    if (!flagged) return;
-    int32_t* const list = plan + guard_list_offset(heads);
-    __syncthreads();
-    // ---- write the rows in order: kUnits consecutive units per thread -----
-    constexpr int kUnits = 4;
-    for (int64_t c0 = 0; c0 < units; c0 += (int64_t)kGuardPlanThreads * kUnits) {
-        uint32_t bits[kUnits];
-        int head[kUnits], head_row[kUnits];
-        bool mine = false;
-#pragma unroll
-        for (int i = 0; i < kUnits; ++i) {
-            const int64_t u = c0 + (int64_t)tid * kUnits + i;
-            bits[i] = 0;
-            head[i] = -1;
-            head_row[i] = 0;
-            if (u < units) bits[i] = load_unit(u, head[i], head_row[i]);
-            mine |= bits[i] != 0;
-        }
-        if (!__syncthreads_or(mine)) continue;
-        for (int h = 0; h < heads; ++h) {
-            int count = 0;
-#pragma unroll
-            for (int i = 0; i < kUnits; ++i) count += head[i] == h ? __builtin_popcount(bits[i]) : 0;
-            int total;
-            const int pos = block_exclusive_scan(count, wave_sum, total);
-            if (count) {
-                int k = next[h] + pos;
-#pragma unroll
-                for (int i = 0; i < kUnits; ++i)
-                    if (head[i] == h)
-                        for (uint32_t b = bits[i]; b; b &= b - 1) list[k++] = head_row[i] + __builtin_ctz(b);
-            }
-            __syncthreads();  // every read of next[h] is done
-            if (tid == 0) next[h] += total;
+    for (int i = 0; i < kGuardListRows; ++i) {
+        int head;
+        const int head_row = guard_head_row(g, row0 + i, head);
+        if (m[i] < thr[head]) {
+            const int pos = atomicAdd(&plan[head], 1);
+            list[head * segment + pos] = head_row;
         }
     }
 }
@@ -219,23 +140,33 @@ __global__ void __launch_bounds__(kGuardMergeThreads) guard_merge_kernel(const f
 
 // ---- V statistics and the guard threshold -------------------------------
 //
-// Layout of the statistics (64-bit words, zeroed by workgroup 0 of the e4m3
-// pass): [h][d] sum of the sampled V codes times 2^9 (two's complement),
-// [h][d] sum of their squares times 2^18, [h] sampled keys, one arrival
-// counter; then the thresholds, one float per KV head.  Every e4m3 value is
-// a multiple of 2^-9 of magnitude at most 448, so the sums are exact
-// integers and the result does not depend on the order the workgroups add
-// them in.
+// guard_vstats_kernel: workgroup (group g, KV head h) sums, per channel d,
+// the sampled V codes of its share of the walk (times 2^9) and their
+// squares (times 2^18) and stores the two int64 rows and its key count in
+// its slot [g][h] of the statistics (plain stores: every slot is written on
+// every call, so nothing needs zeroing).  guard_threshold_kernel then sums
+// the groups' slots per (h, d) and takes the largest variance over d.  Every
+// e4m3 value is a multiple of 2^-9 of magnitude at most 448: the sums of
+// the codes are exact; the squares are summed in fp32 over a thread's few
+// keys and rounded to 2^-18 units before the integer sums, so the result
+// does not depend on the order in which workgroups finish.
 constexpr int kVStatsThreads = 256;
 // Keys per KV head the statistics sample at most (every s-th key of each
 // page, s the smallest power of two that keeps the walk's valid keys / s
 // within it; all keys of a shorter history).
-constexpr int kVStatsKeys = 16384;
-// Workgroups per KV head (at most one per table entry).
-constexpr int kVStatsSlots = 128;
+constexpr int kVStatsKeys = 8192;
+// Workgroups per KV head, table entries one workgroup takes at most, and the
+// 16-byte loads a thread keeps in flight.
+constexpr int kVStatsGroups = 64;
+constexpr int kVStatsEntries = 256;
+constexpr int kVStatsBatch = 8;
+// Channels and threads per workgroup of guard_threshold_kernel.
+constexpr int kVStatsFinalChannels = 64;
+constexpr int kVStatsFinalThreads = 1024;
 
-__host__ __device__ __forceinline__ int vstats_words(int num_kv_heads, int head_dim) {
-    return num_kv_heads * (2 * head_dim + 1) + 1;
+// 64-bit words of the statistics: groups x heads slots of 2 D + 1 words.
+__host__ __device__ __forceinline__ int64_t vstats_words(int groups, int num_kv_heads, int head_dim) {
+    return (int64_t)groups * num_kv_heads * (2 * head_dim + 1);
 }
 
 struct VStatsArgs {
@@ -249,128 +180,231 @@ struct VStatsArgs {
     int32_t num_pages;
     int32_t block_size;
     int32_t num_kv_heads;
-    uint64_t* stats;  // vstats_words(num_kv_heads, D) words
-    float* thr;       // [num_kv_heads]
-    float scale;      // PCPA_GUARD_MIN_MASS * v_scale^2 / 2^18 (the squares' fixed point)
+    int32_t groups;             // workgroups per KV head
+    int32_t entries_per_group;  // table entries of one group (<= kVStatsEntries)
+    int32_t parts;              // groups sharing one entry (its sampled keys dealt round-robin)
+    int64_t* stats;             // vstats_words(groups, num_kv_heads, D) words
+    float* thr;                 // [num_kv_heads]
+    float scale;                // PCPA_GUARD_MIN_MASS * v_scale^2 / 2^18 (the squares' fixed point)
 };
 
-// Grid: slots * num_kv_heads workgroups (slots <= kVStatsSlots); workgroup b
-// takes KV head b % num_kv_heads and every slots-th table entry from b /
-// num_kv_heads.  The last workgroup to finish writes every head's threshold
-// PCPA_GUARD_MIN_MASS * v_scale^2 * max_d (E[v_d^2] - E[v_d]^2).
+// Page and valid length of table entry e (0 for an empty or out-of-range
+// entry), read with vector loads (threads take different entries).
+__device__ __forceinline__ int entry_valid(const VStatsArgs& a, int e, int& page) {
+    page = a.block_table[e << a.table_shift];
+    if (a.table_shift && a.block_table[2 * e + 1] != 0) page = -1;
+    const int n = min(a.page_valid_len[e], a.block_size);
+    return n > 0 && (unsigned)page < (unsigned)a.num_pages ? n : 0;
+}
+
+// Grid: groups * num_kv_heads workgroups; workgroup b takes KV head b %
+// num_kv_heads and group g = b / num_kv_heads: the table entries [e0, e0 +
+// entries_per_group) with e0 = (g / parts) * entries_per_group, and of their
+// sampled keys every parts-th one from g % parts.  Thread (key lane kl,
+// chunk c) reads chunk c of the group's keys kl, kl + KL, ..., kVStatsBatch
+// loads at a time.  Workgroup 0 also zeroes the thresholds, which
+// guard_threshold_kernel raises next.
 template <int D>
 __global__ void __launch_bounds__(kVStatsThreads) guard_vstats_kernel(VStatsArgs a) {
     constexpr int CH = D / 16;                // 16-byte chunks of a key row
     constexpr int KL = kVStatsThreads / CH;  // keys read per pass
-    __shared__ unsigned long long s1[D], s2[D];
-    __shared__ float wmax[kVStatsThreads / 64];
-    __shared__ int last;
+    constexpr int WAVES = kVStatsThreads / 64;
+    static_assert(CH == 16 || CH == 8 || CH == 4, "16-byte chunks of a 64, 128 or 256 byte row");
+    __shared__ int w1[WAVES][D];      // per-wave sums of the codes (times 2^9)
+    __shared__ int64_t w2[WAVES][D];  // and of their squares (times 2^18)
+    __shared__ int prefix[kVStatsEntries + 1];
+    __shared__ int64_t vbase[kVStatsEntries];
+    __shared__ int wsum[WAVES];
     const int heads = a.num_kv_heads;
     const int head = blockIdx.x % heads;
-    const int slot = blockIdx.x / heads;
-    const int slots = gridDim.x / heads;
-    const int tid = threadIdx.x;
+    const int group = blockIdx.x / heads;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = tid % CH, kl = tid / CH;
-    for (int i = tid; i < D; i += kVStatsThreads) s1[i] = s2[i] = 0;
+    if (blockIdx.x == 0 && tid < heads) a.thr[tid] = 0.f;
 
-    typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
-    const const_i32_ptr table = (const_i32_ptr)a.block_table;
-    const const_i32_ptr lens = (const_i32_ptr)a.page_valid_len;
-    // the sampling stride, from the walk's valid keys
+    // ---- the sampling stride, from the walk's valid keys -------------------
     int total = 0;
-    for (int e = 0; e < a.num_entries; ++e) {
-        const int page = table_page(table, e, a.table_shift);
-        const int n = min(lens[e], a.block_size);
-        if (n > 0 && (unsigned)page < (unsigned)a.num_pages) total += n;
+    for (int e = tid; e < a.num_entries; e += kVStatsThreads) {
+        int page;
+        total += entry_valid(a, e, page);
     }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) total += __shfl_xor(total, off);
+    if (lane == 0) wsum[wave] = total;
+    // ---- this group's entries: its sampled keys per entry (prefix) ----------
+    const int part = group % a.parts;
+    const int e0 = group / a.parts * a.entries_per_group;
+    const int ne = max(0, min(a.num_entries - e0, a.entries_per_group));
+    __syncthreads();
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) total += wsum[w];
     int stride = 1;
     while (total / stride > kVStatsKeys) stride <<= 1;
-
-    int acc1[16];
-    unsigned long long acc2[16];
-#pragma unroll
-    for (int b = 0; b < 16; ++b) {
-        acc1[b] = 0;
-        acc2[b] = 0;
+    if (tid < ne) {
+        int page;
+        const int n = entry_valid(a, e0 + tid, page);
+        const int sampled = (n + stride - 1) / stride;  // this entry's keys 0, s, 2s, ...
+        prefix[tid + 1] = sampled > part ? (sampled - part + a.parts - 1) / a.parts : 0;
+        vbase[tid] = n ? (int64_t)page * a.page_stride + (int64_t)(heads + head) * a.head_stride : 0;
     }
-    int count = 0;
-    for (int e = slot; e < a.num_entries; e += slots) {
-        const int page = table_page(table, e, a.table_shift);
-        const int n = min(lens[e], a.block_size);
-        if (n <= 0 || (unsigned)page >= (unsigned)a.num_pages) continue;
-        count += (n + stride - 1) / stride;
-        const uint8_t* const vbase =
-            a.kv + (int64_t)page * a.page_stride + (int64_t)(heads + head) * a.head_stride + c * 16;
-        for (int key = kl * stride; key < n; key += KL * stride) {
-            const v4i x = *(const v4i*)(vbase + (int64_t)key * D);
-            auto add = [&](int b, float v) {
-                // v * 2^9 is an integer of magnitude <= 229376
-                const float y = v * 512.f;
-                const unsigned uv = (unsigned)fabsf(y);
-                acc1[b] += (int)y;
-                acc2[b] += (unsigned long long)uv * uv;
-            };
+    __syncthreads();
+    if (tid == 0) {
+        prefix[0] = 0;
+        for (int i = 0; i < ne; ++i) prefix[i + 1] += prefix[i];
+    }
+    __syncthreads();
+    const int keys = prefix[ne];
+
+    // ---- per-thread sums of chunk c over its keys (fp32) --------------------
+    float f1[16], f2[16];
+#pragma unroll
+    for (int b = 0; b < 16; ++b) f1[b] = f2[b] = 0.f;
+    int entry = 0;  // the entry of this thread's next key (its keys ascend)
+    for (int q0 = kl; q0 < keys; q0 += KL * kVStatsBatch) {
+        v4i x[kVStatsBatch];
+#pragma unroll
+        for (int j = 0; j < kVStatsBatch; ++j) {
+            const int q = q0 + j * KL;
+            x[j] = v4i{0, 0, 0, 0};
+            if (q < keys) {
+                while (q >= prefix[entry + 1]) ++entry;
+                const int key = ((q - prefix[entry]) * a.parts + part) * stride;
+                x[j] = *(const v4i*)(a.kv + vbase[entry] + (int64_t)key * D + c * 16);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kVStatsBatch; ++j)
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(x[w], false);
-                const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(x[w], true);
-                add(4 * w + 0, lo[0]);
-                add(4 * w + 1, lo[1]);
-                add(4 * w + 2, hi[0]);
-                add(4 * w + 3, hi[1]);
+                const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(x[j][w], false);
+                const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(x[j][w], true);
+                const float v[4] = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    f1[4 * w + i] += v[i];
+                    f2[4 * w + i] = fmaf(v[i], v[i], f2[4 * w + i]);
+                }
             }
-        }
     }
-    __syncthreads();  // s1 / s2 zeroed
+    // ---- to fixed point, then the lanes of one chunk: l ^ {CH .. 8} by
+    // shuffles, l ^ 16, l ^ 32 by lane swaps; then the waves through LDS ------
+    // (|sum of codes| <= 448 * keys per thread: exact in fp32 for up to
+    // 2^24 / 229376 = 73 keys a thread, which the sampling cap keeps)
+    auto swap_sum64 = [](int64_t x) -> int64_t {
+        auto pair_sum = [](auto r_lo, auto r_hi) -> int64_t {
+            return (int64_t)((uint64_t)r_hi[0] << 32 | r_lo[0]) + (int64_t)((uint64_t)r_hi[1] << 32 | r_lo[1]);
+        };
+        const uint32_t l0 = (uint32_t)x, h0 = (uint32_t)((uint64_t)x >> 32);
+        const int64_t y = pair_sum(__builtin_amdgcn_permlane16_swap(l0, l0, false, false),
+                                   __builtin_amdgcn_permlane16_swap(h0, h0, false, false));
+        const uint32_t l1 = (uint32_t)y, h1 = (uint32_t)((uint64_t)y >> 32);
+        return pair_sum(__builtin_amdgcn_permlane32_swap(l1, l1, false, false),
+                        __builtin_amdgcn_permlane32_swap(h1, h1, false, false));
+    };
 #pragma unroll
     for (int b = 0; b < 16; ++b) {
-        atomicAdd(&s1[c * 16 + b], (unsigned long long)(long long)acc1[b]);
-        atomicAdd(&s2[c * 16 + b], acc2[b]);
-    }
-    __syncthreads();
-    uint64_t* const sum1 = a.stats + (int64_t)head * D;
-    uint64_t* const sum2 = a.stats + (int64_t)(heads + head) * D;
-    uint64_t* const keys = a.stats + (int64_t)2 * heads * D;
-    uint64_t* const arrivals = keys + heads;
-    for (int i = tid; i < D; i += kVStatsThreads) {
-        atomicAdd((unsigned long long*)&sum1[i], s1[i]);
-        atomicAdd((unsigned long long*)&sum2[i], s2[i]);
-    }
-    if (tid == 0) atomicAdd((unsigned long long*)&keys[head], (unsigned long long)count);
-    // the last workgroup to arrive sees every other one's sums
-    __threadfence();
-    __syncthreads();
-    if (tid == 0)
-        last = atomicAdd((unsigned long long*)arrivals, 1ull) == (unsigned long long)(gridDim.x - 1);
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    for (int h = 0; h < heads; ++h) {
-        const uint64_t nk = __hip_atomic_load(&a.stats[(int64_t)2 * heads * D + h], __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-        float vmax = 0.f;
-        for (int i = tid; i < D; i += kVStatsThreads) {
-            const long long q1 = (long long)__hip_atomic_load(&a.stats[(int64_t)h * D + i], __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT);
-            const uint64_t q2 = __hip_atomic_load(&a.stats[(int64_t)(heads + h) * D + i], __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-            if (nk > 0) {
-                // Var = E[y^2] - E[y]^2 in units of 2^-18 (y = v * 2^9), in double
-                const double mean = (double)q1 / (double)nk;
-                const double var = (double)q2 / (double)nk - mean * mean;
-                vmax = fmaxf(vmax, (float)(var > 0.0 ? var : 0.0));
+        int64_t i1 = (int64_t)(f1[b] * 512.f);
+        int64_t i2 = (int64_t)rint((double)f2[b] * 262144.0);
+        if constexpr (CH < 16) {
+#pragma unroll
+            for (int off = CH; off < 16; off <<= 1) {
+                i1 += __shfl_xor(i1, off);
+                i2 += __shfl_xor(i2, off);
             }
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, off));
-        if ((tid & 63) == 0) wmax[tid >> 6] = vmax;
-        __syncthreads();
-        if (tid == 0) {
-            float m = wmax[0];
-            for (int w = 1; w < kVStatsThreads / 64; ++w) m = fmaxf(m, wmax[w]);
-            a.thr[h] = m * a.scale;
+        i1 = swap_sum64(i1);
+        i2 = swap_sum64(i2);
+        if (lane < CH) {
+            w1[wave][c * 16 + b] = (int)i1;
+            w2[wave][c * 16 + b] = i2;
         }
-        __syncthreads();
+    }
+    __syncthreads();
+    int64_t* const slot = a.stats + ((int64_t)group * heads + head) * (2 * D + 1);
+    for (int i = tid; i < D; i += kVStatsThreads) {
+        int64_t t1 = 0, t2 = 0;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            t1 += w1[w][i];
+            t2 += w2[w][i];
+        }
+        slot[i] = t1;
+        slot[D + i] = t2;
+    }
+    if (tid == 0) slot[2 * D] = keys;
+}
+
+// Grid: num_kv_heads * (D / kVStatsFinalChannels) workgroups of
+// kVStatsFinalThreads; workgroup (h, channel block) sums its channels' slots
+// over the groups (kVStatsFinalThreads / kVStatsFinalChannels threads per
+// channel, four groups' loads in flight at a time), and raises thr[h] to
+// PCPA_GUARD_MIN_MASS * v_scale^2 * its largest variance (non-negative
+// floats order like their bits, so the result does not depend on the order
+// of the workgroups).
+template <int D>
+__global__ void __launch_bounds__(kVStatsFinalThreads) guard_threshold_kernel(VStatsArgs a) {
+    constexpr int PER = kVStatsFinalThreads / kVStatsFinalChannels;  // threads per channel
+    __shared__ int64_t t1[kVStatsFinalThreads], t2[kVStatsFinalThreads];
+    __shared__ int64_t nk_part[kVStatsFinalThreads];
+    __shared__ float vmax[kVStatsFinalChannels];
+    const int blocks = D / kVStatsFinalChannels;
+    const int h = blockIdx.x / blocks;
+    const int d = (blockIdx.x % blocks) * kVStatsFinalChannels + threadIdx.x % kVStatsFinalChannels;
+    const int sub = threadIdx.x / kVStatsFinalChannels;
+    const int heads = a.num_kv_heads;
+    const int64_t slot_words = 2 * D + 1, group_words = (int64_t)heads * slot_words;
+    const int64_t* const base = a.stats + (int64_t)h * slot_words;
+    int64_t s1 = 0, s2 = 0, nk = 0;
+    int g = sub;
+    for (; g + 3 * PER < a.groups; g += 4 * PER) {
+        int64_t x1[4], x2[4], xn[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int64_t* const slot = base + (g + k * PER) * group_words;
+            x1[k] = slot[d];
+            x2[k] = slot[D + d];
+            xn[k] = slot[2 * D];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            s1 += x1[k];
+            s2 += x2[k];
+            nk += xn[k];
+        }
+    }
+    for (; g < a.groups; g += PER) {
+        const int64_t* const slot = base + g * group_words;
+        s1 += slot[d];
+        s2 += slot[D + d];
+        nk += slot[2 * D];
+    }
+    t1[threadIdx.x] = s1;
+    t2[threadIdx.x] = s2;
+    nk_part[threadIdx.x] = nk;
+    __syncthreads();
+    if (threadIdx.x < kVStatsFinalChannels) {
+        int64_t q1 = 0, q2 = 0, n = 0;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            q1 += t1[threadIdx.x + k * kVStatsFinalChannels];
+            q2 += t2[threadIdx.x + k * kVStatsFinalChannels];
+            n += nk_part[threadIdx.x + k * kVStatsFinalChannels];
+        }
+        float var = 0.f;
+        if (n > 0) {
+            // Var = E[y^2] - E[y]^2 in units of 2^-18 (y = v * 2^9), in double
+            const double mean = (double)q1 / (double)n;
+            const double v = (double)q2 / (double)n - mean * mean;
+            var = v > 0.0 ? (float)v : 0.f;
+        }
+        vmax[threadIdx.x] = var;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float m = 0.f;
+        for (int i = 0; i < kVStatsFinalChannels; ++i) m = fmaxf(m, vmax[i]);
+        atomicMax((unsigned*)&a.thr[h], __float_as_uint(m * a.scale));
     }
 }
 

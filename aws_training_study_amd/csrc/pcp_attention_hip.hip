@@ -77,6 +77,7 @@ inline FwdArgs common_args(const pcpa_params* p, const void* q, void* out) {
 struct WorkspaceLayout {
     int64_t part_o, part_lse, part_m, vstats, thr, mass, plan, gpart_o, gpart_lse, bytes;
     int32_t guard_splits, guard_slots, groups_total;
+    int32_t vs_groups, vs_entries_per_group, vs_parts;  // guard_vstats_kernel's work split
 };
 
 // A launch runs e4m3 MFMAs on an e4m3 cache unless PCPA_FLAG_BF16_MFMA.
@@ -116,8 +117,21 @@ inline WorkspaceLayout workspace_layout(const pcpa_params* p, int splits) {
         w.guard_splits = (int32_t)gs;
         const int64_t slots = kGuardPartialRows / kRowsPerGroup / gs;
         w.guard_slots = (int32_t)(slots < w.groups_total ? slots : w.groups_total);
+        // the V statistics: kVStatsGroups workgroups per KV head, each over
+        // whole table entries, or over every parts-th key of fewer entries
+        if (entries >= kVStatsGroups) {
+            int64_t epg = (entries + kVStatsGroups - 1) / kVStatsGroups;
+            epg = epg > kVStatsEntries ? kVStatsEntries : epg;
+            w.vs_entries_per_group = (int32_t)epg;
+            w.vs_parts = 1;
+            w.vs_groups = (int32_t)((entries + epg - 1) / epg);
+        } else {
+            w.vs_entries_per_group = 1;
+            w.vs_parts = (int32_t)(kVStatsGroups / entries);
+            w.vs_groups = (int32_t)(entries * w.vs_parts);
+        }
         w.vstats = align16(w.bytes);
-        w.thr = w.vstats + (int64_t)vstats_words(p->num_kv_heads, p->head_dim) * 8;
+        w.thr = w.vstats + vstats_words(w.vs_groups, p->num_kv_heads, p->head_dim) * 8;
         w.mass = align16(w.thr + (int64_t)p->num_kv_heads * 4);
         w.plan = align16(w.mass + (splits == 1 ? rows * 4 : 0));
         w.gpart_o = align16(w.plan + ((int64_t)guard_list_offset(p->num_kv_heads) +
@@ -221,12 +235,9 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
     const int rows_per_group = overlap ? ovl::kRowsPerGroup : kRowsPerGroup;
     a.row_tiles = (a.rows_per_head + rows_per_group - 1) / rows_per_group;
     const void* fn = nullptr;
-    if (guard) {
-        a.vstats_zero = (uint64_t*)(ws + w.vstats);
-        a.vstats_words = vstats_words(p->num_kv_heads, p->head_dim);
-    }
     if (splits == 1) {
         a.guard_mass = mass;
+        a.guard_zero = plan;  // the listing appends with device atomics
         if (overlap) {
             // the log-sum-exp instantiation also writes the guard's row masses
             const bool aux = lse || mass;
@@ -278,16 +289,24 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
         v.num_pages = a.num_pages;
         v.block_size = a.block_size;
         v.num_kv_heads = a.num_kv_heads;
-        v.stats = (uint64_t*)(ws + w.vstats);
+        v.stats = (int64_t*)(ws + w.vstats);
         v.thr = thr;
         v.scale = PCPA_GUARD_MIN_MASS * p->v_scale * p->v_scale / 262144.f;
-        const int slots = a.num_entries < kVStatsSlots ? a.num_entries : kVStatsSlots;
+        v.groups = w.vs_groups;
+        v.entries_per_group = w.vs_entries_per_group;
+        v.parts = w.vs_parts;
         const void* vfn = p->head_dim == 64    ? (const void*)guard_vstats_kernel<64>
                           : p->head_dim == 128 ? (const void*)guard_vstats_kernel<128>
                                                : (const void*)guard_vstats_kernel<256>;
+        const void* tfn = p->head_dim == 64    ? (const void*)guard_threshold_kernel<64>
+                          : p->head_dim == 128 ? (const void*)guard_threshold_kernel<128>
+                                               : (const void*)guard_threshold_kernel<256>;
         void* vargs[] = {&v};
-        if (hipLaunchKernel(vfn, dim3(slots * p->num_kv_heads), dim3(kVStatsThreads), vargs, 0, stream) !=
+        if (hipLaunchKernel(vfn, dim3(v.groups * p->num_kv_heads), dim3(kVStatsThreads), vargs, 0, stream) !=
             hipSuccess)
+            return PCPA_ERR_LAUNCH;
+        if (hipLaunchKernel(tfn, dim3(p->num_kv_heads * (p->head_dim / kVStatsFinalChannels)),
+                            dim3(kVStatsFinalThreads), vargs, 0, stream) != hipSuccess)
             return PCPA_ERR_LAUNCH;
     }
     if (splits > 1) {
@@ -306,8 +325,9 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
         // the exactly widened cache): plan (one pass; a split launch's merge
         // listed the rows), fixup, merge of its ranges
         if (splits == 1) {
-            hipLaunchKernelGGL(guard_plan_kernel, dim3(1), dim3(kGuardPlanThreads), 0, stream,
-                               (const float*)mass, (const float*)thr, g, plan);
+            const int64_t per_group = (int64_t)kGuardListRows * kGuardListThreads;
+            hipLaunchKernelGGL(guard_list_kernel, dim3((unsigned)((g.rows_total + per_group - 1) / per_group)),
+                               dim3(kGuardListThreads), 0, stream, (const float*)mass, (const float*)thr, g, plan);
             if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
         }
         FwdArgs b = history_args(p, q, kv_pages, block_table, page_valid_len, out, lse);
