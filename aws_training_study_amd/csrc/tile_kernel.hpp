@@ -223,6 +223,13 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, uint32_t rt_off
         }
     }
 
+    // Wave priority: the two waves a SIMD holds run the same loop out of
+    // phase.  Four-wave workgroups (two per CU, a SIMD's waves from
+    // different workgroups) finish sooner when the wave in its softmax
+    // issues first (GQA-8 workload 2.018 vs 2.040 ms); key-split pairs
+    // (the two waves of one pair on a SIMD) when the wave at its MFMAs does
+    // (64-rank BF16 cache 16.43 vs 16.62 ms; interleaved runs on one box).
+    __builtin_amdgcn_s_setprio(S::PAIR ? 0 : 1);
     // ---- mask, online softmax (lazy rescale) ----------------------------
     // (CAUSAL: only tiles that cross some row's limit, a wave-uniform test)
     constexpr int KEYS = 32 * S::NT;  // keys of the tile this wave scores
@@ -269,6 +276,7 @@ __device__ __forceinline__ void compute_tile(const uint8_t* lds, uint32_t rt_off
     // the e4m3-rounded P that the PV MFMAs consume, taken by an MFMA below.
     if constexpr (!FP8) st.l += psum;
 
+    __builtin_amdgcn_s_setprio(S::PAIR ? 1 : 0);
     // ---- O^T += V^T . P^T -----------------------------------------------
     if constexpr (FP8) {
         v8i pop;
