@@ -70,24 +70,22 @@ struct FwdArgs {
     float* part_o;            // [splits, pcp * Hq * local_q, D] fp32 (or fp16)
     float* part_lse;          // [splits, pcp * Hq * local_q]
     float* part_m;            // [splits, pcp * Hq * local_q]: each range's reference max (log2)
-    // Precision guard of the e4m3-MFMA kernels.  guard_mass (one float per
-    // row, [pcp, Hq, local_q]): the one-pass e4m3 kernel writes each row's
-    // probability mass sum_k 2^(x_k - m); the guard plan lists the rows below
-    // their KV head's threshold (guard_vstats_kernel).  A split launch
-    // instead sets the row counts of the guard plan guard_zero to 0
-    // (workgroup 0), and its merge appends the rows; a one-pass launch's
-    // guard_list_kernel does the same after it.
-    float* guard_mass;
-    int32_t* guard_zero;
+    // Precision guard of a one-pass e4m3-MFMA launch: each row whose
+    // probability mass sum_k 2^(x_k - m) is below its KV head's threshold
+    // (guard_threshold over guard_thr, written by guard_vstats_kernel, which
+    // also zeroed the plan's row counts) is appended to the guard plan
+    // guard_rows.  A split launch leaves both null; its merge appends.
+    const float* guard_thr;
+    int32_t* guard_rows;
     // The BF16 fixup of a guarded launch (history_fwd_kernel<..., FIXUP>):
-    // the guard plan (below) and the partials' capacity in 128-row groups
-    // (part_o / part_lse hold [splits, guard_slots * 128] rows): with at
-    // most guard_slots groups the fixup is sparse (each group's history walk
-    // split over `splits` workgroups, partials merged by guard_merge_kernel),
-    // with more it is dense (one workgroup per group, output written
-    // directly).
+    // the guard plan (below), the partials' capacity in rows (part_o /
+    // part_lse) and, in `splits`, the most history ranges a group is cut
+    // into.  guard_ranges() picks the ranges for the number of groups
+    // listed: with two or more the fixup is sparse (each group's walk split
+    // over that many workgroups, partials merged by guard_merge_kernel),
+    // else dense (one workgroup per group, output written directly).
     const int32_t* guard_plan;
-    int32_t guard_slots;
+    int32_t guard_partial_rows;
 };
 
 // A guard plan: [h] (h < num_kv_heads) the number of flagged rows of KV head
@@ -111,14 +109,34 @@ struct GuardShape {
     int32_t num_q_heads;
     int32_t num_kv_heads;
     int32_t group;
-    int32_t max_sparse;   // 128-row groups the sparse partials hold
+    int32_t partial_rows;  // rows the sparse fixup's partials hold
+    int32_t max_ranges;    // history ranges a sparse group is cut into at most
 };
 
-// Workgroup 0 of a guarded e4m3 launch: the guard plan's row counts start
-// at zero (the merge of a split launch, or guard_list_kernel after a
-// one-pass launch, appends the rows).
-__device__ __forceinline__ void guard_zero_counts(const FwdArgs& a) {
-    if (a.guard_zero && (int)threadIdx.x < a.num_kv_heads) a.guard_zero[threadIdx.x] = 0;
+// History ranges of a sparse fixup over `groups` listed 128-row groups: as
+// many as the partials hold (partial_rows rows), at most max_ranges; 0
+// (dense: one workgroup per group) when fewer than two fit.
+__host__ __device__ __forceinline__ int guard_ranges(int groups, int partial_rows, int max_ranges) {
+    if (groups <= 0) return 0;
+    int r = partial_rows / (kRowsPerGroup * groups);
+    r = r < max_ranges ? r : max_ranges;
+    return r >= 2 ? r : 0;
+}
+
+// The threshold of KV head `head`: the largest of its `chunks` (head_dim /
+// 16) per-chunk values (guard_vstats_kernel).
+__device__ __forceinline__ float guard_threshold(const float* thr, int head, int chunks) {
+    float t = 0.f;
+#pragma unroll 16
+    for (int c = 0; c < chunks; ++c) t = fmaxf(t, thr[head * chunks + c]);
+    return t;
+}
+
+// Append head row `row` to KV head `head`'s list of the guard plan (its
+// count was zeroed by guard_vstats_kernel earlier in the launch).
+__device__ __forceinline__ void guard_append(int32_t* plan, int num_kv_heads, int rows_per_head, int head, int row) {
+    const int pos = atomicAdd(&plan[head], 1);
+    plan[guard_list_offset(num_kv_heads) + head * guard_head_segment(rows_per_head) + pos] = row;
 }
 
 // Flag-array index ([pcp, Hq, local_q] order) of row r of KV head `head`.
@@ -388,35 +406,62 @@ __device__ __forceinline__ TileCursor next_tile(const FwdArgs& a, int head, Tile
     return TileCursor{a.num_entries, 0, 0, 0};
 }
 
-// Key tiles of the whole walk (every entry with valid tokens and an in-range
-// page contributes ceil(n / 64)).
-__device__ __forceinline__ int walk_tiles(const FwdArgs& a) {
-    typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
-    const const_i32_ptr table = (const_i32_ptr)a.block_table;
-    const const_i32_ptr lens = (const_i32_ptr)a.page_valid_len;
-    int total = 0;
-    for (int e = 0; e < a.num_entries; ++e) {
-        const int page = table_page(table, e, a.table_shift);
-        const int n = min(lens[e], a.block_size);
-        if (n > 0 && (unsigned)page < (unsigned)a.num_pages) total += (n + kKeyTile - 1) / kKeyTile;
+// For a whole workgroup of T threads at once: the cursor of the first key
+// tile of range `split` of `splits` equal ranges of the walk's key tiles
+// (every entry with valid tokens and an in-range page contributes
+// ceil(n / 64)), and in `tiles` the range's tile count (the end cursor for
+// an empty range).  Thread t counts the tiles of its block
+// of consecutive entries, a scan over the workgroup (`red`: one int per
+// wave) places the blocks, and the block holding the range's first tile
+// finds its entry and writes the cursor to `shared`.  Every thread of the
+// workgroup must call it.
+template <int T>
+__device__ __forceinline__ TileCursor range_cursor(const FwdArgs& a, int head, int split, int splits, int& tiles,
+                                                   int* red, TileCursor* shared) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int per = (a.num_entries + T - 1) / T;
+    const int e_lo = min(tid * per, a.num_entries), e_hi = min(e_lo + per, a.num_entries);
+    int cnt = 0;
+    for (int e = e_lo; e < e_hi; ++e) {
+        const int page = table_page(a.block_table, e, a.table_shift);
+        const int n = min(a.page_valid_len[e], a.block_size);
+        if (n > 0 && (unsigned)page < (unsigned)a.num_pages) cnt += (n + kKeyTile - 1) / kKeyTile;
     }
-    return total;
-}
-
-// The cursor of key tile t of the walk (the end cursor past its last tile).
-__device__ __forceinline__ TileCursor cursor_at_tile(const FwdArgs& a, int head, int t) {
-    typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
-    const const_i32_ptr table = (const_i32_ptr)a.block_table;
-    const const_i32_ptr lens = (const_i32_ptr)a.page_valid_len;
-    for (int e = 0; e < a.num_entries; ++e) {
-        const int page = table_page(table, e, a.table_shift);
-        const int n = min(lens[e], a.block_size);
-        if (n <= 0 || (unsigned)page >= (unsigned)a.num_pages) continue;
-        const int tiles = (n + kKeyTile - 1) / kKeyTile;
-        if (t < tiles) return TileCursor{e, t * kKeyTile, n, (int64_t)page * a.page_stride + (int64_t)head * a.head_stride};
-        t -= tiles;
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off);
+        if (lane >= off) incl += y;
     }
-    return TileCursor{a.num_entries, 0, 0, 0};
+    if (lane == 63) red[wave] = incl;
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < T / 64; ++w) {
+        before += w < wave ? red[w] : 0;
+        total += red[w];
+    }
+    const int first = (int)((int64_t)total * split / splits);
+    tiles = (int)((int64_t)total * (split + 1) / splits) - first;
+    if (tiles <= 0) return TileCursor{a.num_entries, 0, 0, 0};  // the same for every thread
+    const int excl = before + incl - cnt;
+    if (first >= excl && first < excl + cnt) {
+        int t = first - excl;
+        for (int e = e_lo; e < e_hi; ++e) {
+            const int page = table_page(a.block_table, e, a.table_shift);
+            const int n = min(a.page_valid_len[e], a.block_size);
+            if (n <= 0 || (unsigned)page >= (unsigned)a.num_pages) continue;
+            const int nt = (n + kKeyTile - 1) / kKeyTile;
+            if (t < nt) {
+                *shared = TileCursor{e, t * kKeyTile, n,
+                                     (int64_t)page * a.page_stride + (int64_t)head * a.head_stride};
+                break;
+            }
+            t -= nt;
+        }
+    }
+    __syncthreads();
+    return *shared;
 }
 
 // The tile after `c` in the single "page" of the current tokens (CAUSAL

@@ -554,8 +554,9 @@ __device__ __forceinline__ int64_t query_row_offset(const FwdArgs& a, int row, i
     return ((int64_t)(rank * a.num_q_heads + head * a.group + head_in_group) * a.local_q + tok) * D * 2;
 }
 
-// LSE: also write each row's log-sum-exp and the precision guard's flag
-// (whichever of a.lse / a.guard_out is set; a separate instantiation, so
+// LSE: also write each row's log-sum-exp and/or list the rows of a
+// precision-guarded launch whose mass is below their KV head's threshold
+// (whichever of a.lse / a.guard_thr is set; a separate instantiation, so
 // that the plain one keeps its register allocation).
 // SPLIT: the workgroup walks only its split's share of the table entries
 // and writes a normalised FP32 partial output and log-sum-exp (merged by
@@ -567,7 +568,6 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
     constexpr int DMAW = kWaves / 2;
     using P = DmaPlan<D, DMAW>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * S::RING];
-    if (blockIdx.x == 0) guard_zero_counts(a);
 
     // ---- XCD-aware work mapping (as history_fwd_kernel) ---------------------
     // Items run row tile fastest, so an XCD's workgroups share one (KV head,
@@ -744,11 +744,12 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
         return;
     }
     if constexpr (LSE) {
-        // the log-sum-exp and/or the precision guard's row mass: l / 2^6 is
-        // the row's probability mass sum_k 2^(x_k - m)
-        if (row_ok && h == 0) {
-            if (a.lse) a.lse[row_off / (D * 2)] = lse;
-            if (a.guard_mass) a.guard_mass[row_off / (D * 2)] = sm.l * (1.f / 64.f);
+        if (a.lse && row_ok && h == 0) a.lse[row_off / (D * 2)] = lse;
+        // precision guard: l / 2^6 is the row's probability mass sum_k 2^(x_k - m)
+        if (a.guard_thr) {
+            const float thr = guard_threshold(a.guard_thr, head, D / 16);
+            if (row_ok && h == 0 && sm.l * (1.f / 64.f) < thr)
+                guard_append(a.guard_rows, a.num_kv_heads, a.rows_per_head, head, row);
         }
     }
     if (row_ok) {
@@ -782,8 +783,9 @@ __global__ void __launch_bounds__(kThreads, 1) history_fwd_overlap(FwdArgs a) {
 // Precision guard (guard_plan set): the row's probability mass against the
 // largest range reference m_ref = max_s part_m, sum_s l_s 2^(m_s - m_ref) / 2^6
 // = e^(lse + lse_bias - m_ref ln 2) (lse_bias: what the kernel subtracted
-// from its log-sum-exps); a row below its KV head's threshold guard_thr
-// (guard_vstats_kernel) is appended to the guard plan.
+// from its log-sum-exps); a row below its KV head's threshold (the largest
+// of the head's D / 16 values in guard_thr, from guard_vstats_kernel, which
+// also zeroed the plan's counts) is appended to the guard plan.
 __global__ void __launch_bounds__(256) merge_splits_kernel(const float* part_o, int part_f16, float part_scale,
                                                            const float* part_lse, int splits, int64_t rows, int d_vec8, uint8_t* out,
                                                            float* lse_out,
@@ -843,12 +845,8 @@ __global__ void __launch_bounds__(256) merge_splits_kernel(const float* part_o, 
         const float mass = wsum > 0.f ? __expf(lse + lse_bias - m_ref * kLn2) : 0.f;
         int head;
         const int head_row = guard_head_row(g, row, head);
-        if (mass < guard_thr[head]) {
-            // append the row to its KV head's list (the split kernel zeroed the counts)
-            const int pos = atomicAdd(&guard_plan[head], 1);
-            guard_plan[guard_list_offset(g.num_kv_heads) + head * guard_head_segment(g.rows_per_head) + pos] =
-                head_row;
-        }
+        if (mass < guard_threshold(guard_thr, head, d_vec8 / 2))
+            guard_append(guard_plan, g.num_kv_heads, g.rows_per_head, head, head_row);
     }
 }
 

@@ -71,13 +71,13 @@ inline FwdArgs common_args(const pcpa_params* p, const void* q, void* out) {
 }
 
 // Workspace of a history launch: split partials (outputs, log-sum-exps and
-// reference maxima of every range) and, for the precision guard, the V
-// statistics and per-head thresholds, the row masses (one pass), the fixup
-// plan and the fixup's split partials.
+// reference maxima of every range) and, for the precision guard, the
+// per-chunk thresholds, the fixup plan and the fixup's range partials.
 struct WorkspaceLayout {
-    int64_t part_o, part_lse, part_m, vstats, thr, mass, plan, gpart_o, gpart_lse, bytes;
-    int32_t guard_splits, guard_slots, groups_total;
-    int32_t vs_groups, vs_entries_per_group, vs_parts;  // guard_vstats_kernel's work split
+    int64_t part_o, part_lse, part_m, thr, plan, gpart_o, gpart_lse, bytes;
+    int32_t groups_total;  // 128-row groups the plan can list
+    int32_t max_ranges;    // history ranges a sparse fixup group is cut into at most
+    int32_t partial_rows;  // rows the fixup's range partials hold
 };
 
 // A launch runs e4m3 MFMAs on an e4m3 cache unless PCPA_FLAG_BF16_MFMA.
@@ -105,40 +105,27 @@ inline WorkspaceLayout workspace_layout(const pcpa_params* p, int splits) {
     }
     if (guarded(p)) {
         // fixup: the flagged rows gathered into groups of 128 (at most as
-        // many groups as 128-row tiles); the history's key tiles cut into
-        // ranges of at least 2 (128 keys), 64 ranges at most, so that a few flagged
-        // rows cost a short walk rather than a whole history's
+        // many groups as 128-row tiles); a sparse group's history walk is
+        // cut into ranges of at least 2 key tiles (128 keys), 64 ranges at
+        // most, so that a few flagged rows cost a short walk rather than a
+        // whole history's; the partials hold kGuardPartialRows rows, which
+        // guard_ranges() shares among the groups listed
         const int64_t entries = (int64_t)p->pcp_size * p->max_local_blocks;
         const int64_t key_tiles = entries * (p->block_size / kKeyTile);
         const int64_t rows_per_head = rows / p->num_q_heads * (p->num_q_heads / p->num_kv_heads);
         w.groups_total = (int32_t)((rows_per_head + kRowsPerGroup - 1) / kRowsPerGroup * p->num_kv_heads);
-        int64_t gs = key_tiles / 2;
-        gs = gs < 1 ? 1 : gs > 64 ? 64 : gs;
-        w.guard_splits = (int32_t)gs;
-        const int64_t slots = kGuardPartialRows / kRowsPerGroup / gs;
-        w.guard_slots = (int32_t)(slots < w.groups_total ? slots : w.groups_total);
-        // the V statistics: kVStatsGroups workgroups per KV head, each over
-        // whole table entries, or over every parts-th key of fewer entries
-        if (entries >= kVStatsGroups) {
-            int64_t epg = (entries + kVStatsGroups - 1) / kVStatsGroups;
-            epg = epg > kVStatsEntries ? kVStatsEntries : epg;
-            w.vs_entries_per_group = (int32_t)epg;
-            w.vs_parts = 1;
-            w.vs_groups = (int32_t)((entries + epg - 1) / epg);
-        } else {
-            w.vs_entries_per_group = 1;
-            w.vs_parts = (int32_t)(kVStatsGroups / entries);
-            w.vs_groups = (int32_t)(entries * w.vs_parts);
-        }
-        w.vstats = align16(w.bytes);
-        w.thr = w.vstats + vstats_words(w.vs_groups, p->num_kv_heads, p->head_dim) * 8;
-        w.mass = align16(w.thr + (int64_t)p->num_kv_heads * 4);
-        w.plan = align16(w.mass + (splits == 1 ? rows * 4 : 0));
+        int64_t mr = key_tiles / 2;
+        mr = mr < 1 ? 1 : mr > 64 ? 64 : mr;
+        w.max_ranges = (int32_t)mr;
+        int64_t prows = mr >= 2 ? (int64_t)w.groups_total * kRowsPerGroup * mr : 0;
+        prows = prows < kGuardPartialRows ? prows : kGuardPartialRows;
+        w.partial_rows = (int32_t)prows;
+        w.thr = align16(w.bytes);
+        w.plan = align16(w.thr + (int64_t)p->num_kv_heads * (p->head_dim / 16) * 4);
         w.gpart_o = align16(w.plan + ((int64_t)guard_list_offset(p->num_kv_heads) +
                                       (int64_t)w.groups_total * kRowsPerGroup) * 4);
-        const int64_t prow = (int64_t)w.guard_splits * w.guard_slots * kRowsPerGroup;
-        w.gpart_lse = w.gpart_o + prow * p->head_dim * 4;
-        w.bytes = w.gpart_lse + prow * 4;
+        w.gpart_lse = w.gpart_o + prows * p->head_dim * 4;
+        w.bytes = w.gpart_lse + prows * 4;
     }
     return w;
 }
@@ -226,21 +213,46 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
     }
     if (w.bytes > 0 && (!workspace || workspace_bytes < w.bytes)) return PCPA_ERR_WORKSPACE;
     uint8_t* const ws = (uint8_t*)workspace;
-    float* const mass = guard && splits == 1 ? (float*)(ws + w.mass) : nullptr;
     int32_t* const plan = guard ? (int32_t*)(ws + w.plan) : nullptr;
     float* const thr = guard ? (float*)(ws + w.thr) : nullptr;
     const bool fast = !(p->flags & PCPA_FLAG_EXACT_EXP2);
 
     FwdArgs a = history_args(p, q, kv_pages, block_table, page_valid_len, out, lse);
+    if (guard) {
+        // first the V statistics of the walk: each KV head's threshold (per
+        // 16-channel chunk), and the guard plan's row counts set to zero
+        VStatsArgs v{};
+        v.kv = a.kv;
+        v.block_table = a.block_table;
+        v.page_valid_len = a.page_valid_len;
+        v.page_stride = a.page_stride;
+        v.head_stride = a.head_stride;
+        v.num_entries = a.num_entries;
+        v.table_shift = a.table_shift;
+        v.num_pages = a.num_pages;
+        v.block_size = a.block_size;
+        v.num_kv_heads = a.num_kv_heads;
+        v.thr = thr;
+        v.plan = plan;
+        v.scale = PCPA_GUARD_MIN_MASS * p->v_scale * p->v_scale / 262144.f;
+        const void* vfn = p->head_dim == 64    ? (const void*)guard_vstats_kernel<64>
+                          : p->head_dim == 128 ? (const void*)guard_vstats_kernel<128>
+                                               : (const void*)guard_vstats_kernel<256>;
+        void* vargs[] = {&v};
+        const int chunks = p->num_kv_heads * (p->head_dim / 16);
+        if (hipLaunchKernel(vfn, dim3(8 * ((chunks + 7) / 8)), dim3(kVStatsThreads), vargs, 0, stream) != hipSuccess)
+            return PCPA_ERR_LAUNCH;
+    }
     const int rows_per_group = overlap ? ovl::kRowsPerGroup : kRowsPerGroup;
     a.row_tiles = (a.rows_per_head + rows_per_group - 1) / rows_per_group;
     const void* fn = nullptr;
     if (splits == 1) {
-        a.guard_mass = mass;
-        a.guard_zero = plan;  // the listing appends with device atomics
+        // a guarded pass lists its rows below the threshold itself
+        a.guard_thr = thr;
+        a.guard_rows = plan;
         if (overlap) {
-            // the log-sum-exp instantiation also writes the guard's row masses
-            const bool aux = lse || mass;
+            // the log-sum-exp instantiation also lists the guard's rows
+            const bool aux = lse || guard;
             fn = fast ? (aux ? (const void*)ovl::history_fwd_overlap<256, true, true>
                              : (const void*)ovl::history_fwd_overlap<256, true, false>)
                       : (aux ? (const void*)ovl::history_fwd_overlap<256, false, true>
@@ -254,7 +266,6 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
         a.part_f16 = f16_partials(p) ? 1 : 0;
         a.part_lse = (float*)(ws + w.part_lse);
         a.part_m = guard ? (float*)(ws + w.part_m) : nullptr;
-        a.guard_zero = plan;
         if (overlap)
             fn = fast ? (const void*)ovl::history_fwd_overlap<256, true, false, true>
                       : (const void*)ovl::history_fwd_overlap<256, false, false, true>;
@@ -275,42 +286,10 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
     g.num_q_heads = a.num_q_heads;
     g.num_kv_heads = a.num_kv_heads;
     g.group = a.group;
-    g.max_sparse = w.guard_slots;
-    if (guard) {
-        // the V statistics of the walk and each KV head's mass threshold
-        VStatsArgs v{};
-        v.kv = a.kv;
-        v.block_table = a.block_table;
-        v.page_valid_len = a.page_valid_len;
-        v.page_stride = a.page_stride;
-        v.head_stride = a.head_stride;
-        v.num_entries = a.num_entries;
-        v.table_shift = a.table_shift;
-        v.num_pages = a.num_pages;
-        v.block_size = a.block_size;
-        v.num_kv_heads = a.num_kv_heads;
-        v.stats = (int64_t*)(ws + w.vstats);
-        v.thr = thr;
-        v.scale = PCPA_GUARD_MIN_MASS * p->v_scale * p->v_scale / 262144.f;
-        v.groups = w.vs_groups;
-        v.entries_per_group = w.vs_entries_per_group;
-        v.parts = w.vs_parts;
-        const void* vfn = p->head_dim == 64    ? (const void*)guard_vstats_kernel<64>
-                          : p->head_dim == 128 ? (const void*)guard_vstats_kernel<128>
-                                               : (const void*)guard_vstats_kernel<256>;
-        const void* tfn = p->head_dim == 64    ? (const void*)guard_threshold_kernel<64>
-                          : p->head_dim == 128 ? (const void*)guard_threshold_kernel<128>
-                                               : (const void*)guard_threshold_kernel<256>;
-        void* vargs[] = {&v};
-        if (hipLaunchKernel(vfn, dim3(v.groups * p->num_kv_heads), dim3(kVStatsThreads), vargs, 0, stream) !=
-            hipSuccess)
-            return PCPA_ERR_LAUNCH;
-        if (hipLaunchKernel(tfn, dim3(p->num_kv_heads * (p->head_dim / kVStatsFinalChannels)),
-                            dim3(kVStatsFinalThreads), vargs, 0, stream) != hipSuccess)
-            return PCPA_ERR_LAUNCH;
-    }
+    g.partial_rows = w.partial_rows;
+    g.max_ranges = w.max_ranges;
     if (splits > 1) {
-        // the merge also lists the guard's rows (the split kernel zeroed the counts)
+        // the merge also lists the guard's rows
         const int d_vec8 = p->head_dim / 8;
         const int64_t threads = g.rows_total * d_vec8;
         hipLaunchKernelGGL(merge_splits_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
@@ -321,24 +300,17 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
         if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
     }
     if (guard) {
-        // the BF16 fixup of the flagged rows' 128-row tiles (BF16 MFMAs over
-        // the exactly widened cache): plan (one pass; a split launch's merge
-        // listed the rows), fixup, merge of its ranges
-        if (splits == 1) {
-            const int64_t per_group = (int64_t)kGuardListRows * kGuardListThreads;
-            hipLaunchKernelGGL(guard_list_kernel, dim3((unsigned)((g.rows_total + per_group - 1) / per_group)),
-                               dim3(kGuardListThreads), 0, stream, (const float*)mass, (const float*)thr, g, plan);
-            if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
-        }
+        // the BF16 fixup of the listed rows' 128-row groups (BF16 MFMAs over
+        // the exactly widened cache), then the merge of its ranges
         FwdArgs b = history_args(p, q, kv_pages, block_table, page_valid_len, out, lse);
         b.row_tiles = (a.rows_per_head + kRowsPerGroup - 1) / kRowsPerGroup;
         b.guard_plan = plan;
-        b.splits = w.guard_splits;
-        b.guard_slots = w.guard_slots;
+        b.splits = w.max_ranges;
+        b.guard_partial_rows = w.partial_rows;
         b.part_o = (float*)(ws + w.gpart_o);
         b.part_lse = (float*)(ws + w.gpart_lse);
         void* bargs[] = {&b};
-        const int sparse_items = w.guard_slots * w.guard_splits;
+        const int sparse_items = w.partial_rows / kRowsPerGroup;  // groups x ranges at most
         const int grid = sparse_items > w.groups_total ? sparse_items : w.groups_total;
         const void* fix = nullptr;
         switch (p->head_dim) {
@@ -349,12 +321,12 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
         }
         if (hipLaunchKernel(fix, dim3(grid), dim3(tile_threads(p->head_dim, false)), bargs, 0, stream) != hipSuccess)
             return PCPA_ERR_LAUNCH;
-        const int d_vec8 = p->head_dim / 8;
-        const int64_t slot_rows = (int64_t)w.guard_slots * kRowsPerGroup;
-        hipLaunchKernelGGL(guard_merge_kernel, dim3((unsigned)slot_rows), dim3(kGuardMergeThreads), 0, stream,
-                           (const float*)b.part_o, (const float*)b.part_lse, w.guard_splits, (const int32_t*)plan, g,
-                           d_vec8, (uint8_t*)out, lse);
-        if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
+        if (w.partial_rows > 0) {
+            hipLaunchKernelGGL(guard_merge_kernel, dim3(kGuardMergeGroups), dim3(kGuardMergeThreads), 0, stream,
+                               (const float*)b.part_o, (const float*)b.part_lse, (const int32_t*)plan, g,
+                               p->head_dim / 8, (uint8_t*)out, lse);
+            if (hipGetLastError() != hipSuccess) return PCPA_ERR_LAUNCH;
+        }
     }
     return PCPA_OK;
 }

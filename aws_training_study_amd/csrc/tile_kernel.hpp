@@ -493,10 +493,11 @@ __device__ __forceinline__ QueryRow query_row(const FwdArgs& a, int head, int ro
 // merge_splits_kernel).
 // FIXUP: the BF16-MFMA pass of a precision-guarded launch.  The guard plan
 // lists the rows the e4m3 pass flagged, in groups of 128 rows of one KV
-// head; in sparse mode (at most guard_slots groups) workgroup b takes group
-// b / splits and walks history range b % splits into the guard partials
-// (merged by guard_merge_kernel), in dense mode it takes group b and writes
-// the output directly; workgroups past the plan exit at once.
+// head; in sparse mode (guard_ranges() >= 2 ranges for the listed groups)
+// workgroup b takes group b / ranges and walks history range b % ranges
+// into the guard partials (merged by guard_merge_kernel), in dense mode it
+// takes group b and writes the output directly; workgroups past the plan
+// exit at once.
 template <int D, bool STORE8, bool FP8, bool CAUSAL = false, bool SPLIT = false, bool FIXUP = false>
 __global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileShape<D, STORE8, FP8>::PAIR ? 1 : 2))
     history_fwd_kernel(FwdArgs a) {
@@ -508,7 +509,6 @@ __global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileSha
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S::LDS_BYTES];
     __shared__ int wave_limit[S::WAVES];
     __shared__ float pair_ml[S::PAIR ? kWaves * 64 * 2 : 1];  // PAIR: the partners' (m, l) per lane
-    if (!FIXUP && !CAUSAL && blockIdx.x == 0) guard_zero_counts(a);
 
     // ---- XCD-aware work mapping ------------------------------------------
     // Workgroups are dealt to the 8 XCDs round-robin by launch index; give
@@ -522,14 +522,15 @@ __global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileSha
     // XCD's workgroups share one (KV head, split) and its pages.
     int splits = SPLIT ? a.splits : 1;
     const int items = a.row_tiles * a.num_kv_heads * splits;
-    int head, row_tile, split = 0, slot = 0, fix_first = 0, fix_count = 0;
+    int head, row_tile, split = 0, slot = 0, fix_first = 0, fix_count = 0, listed = 0;
     bool sparse = false;
     if constexpr (FIXUP) {
-        const int listed = guard_groups(a.guard_plan, a.num_kv_heads);
-        sparse = listed <= a.guard_slots;
+        listed = guard_groups(a.guard_plan, a.num_kv_heads);
+        const int ranges = guard_ranges(listed, a.guard_partial_rows, a.splits);
+        sparse = ranges > 0;
         if (sparse) {
-            if ((int)blockIdx.x >= listed * a.splits) return;
-            splits = a.splits;
+            if ((int)blockIdx.x >= listed * ranges) return;
+            splits = ranges;
             slot = blockIdx.x / splits;
             split = blockIdx.x - slot * splits;
         } else {
@@ -560,12 +561,14 @@ __global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileSha
         a.num_entries = (int)((int64_t)a.num_entries * (split + 1) / splits);
     }
     // FIXUP, sparse: range `split` of `splits` equal ranges of the walk's key
-    // tiles (not of table entries: short ranges even for a few large pages)
-    int tile_first = 0, tiles_left = -1;
-    if (FIXUP && sparse) {
-        const int total = walk_tiles(a);
-        tile_first = (int)((int64_t)total * split / splits);
-        tiles_left = (int)((int64_t)total * (split + 1) / splits) - tile_first;
+    // tiles (not of table entries: short ranges even for a few large pages),
+    // found by the whole workgroup at once
+    int tiles_left = -1;
+    TileCursor range_first{};
+    if constexpr (FIXUP) {
+        __shared__ int walk_red[S::THREADS / 64];
+        __shared__ TileCursor walk_first;
+        if (sparse) range_first = range_cursor<S::THREADS>(a, head, split, splits, tiles_left, walk_red, &walk_first);
     }
 
     const int tid = threadIdx.x;
@@ -705,7 +708,7 @@ __global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileSha
 
     TileCursor cur;
     if (FIXUP && sparse)
-        cur = tiles_left > 0 ? cursor_at_tile(a, head, tile_first) : TileCursor{a.num_entries, 0, 0, 0};
+        cur = range_first;
     else
         cur = advance(TileCursor{entry_begin - 1, 0, 0, 0});
     if constexpr (S::NBUF == 2) {
@@ -776,10 +779,9 @@ __global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileSha
     float lse = l_tot > 0.f ? __logf(l_tot) + (st.m - (FP8 ? kPBiasLog2 : 0.f)) * kLn2 : -INFINITY;
     const int64_t row_index = row_off / (D * 2);
     if (FIXUP && sparse) {
-        // guard partials [splits, slots * 128, D]: slot rows in tile order
+        // guard partials [ranges, listed * 128, D]: slot rows in tile order
         if (row_ok) {
-            const int64_t prow = (int64_t)split * a.guard_slots * kRowsPerGroup + (int64_t)slot * kRowsPerGroup +
-                                 pw * kRowsPerWave + j;
+            const int64_t prow = ((int64_t)split * listed + slot) * kRowsPerGroup + pw * kRowsPerWave + j;
             float* const po = a.part_o + prow * D;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt)
@@ -813,8 +815,13 @@ __global__ void __launch_bounds__((TileShape<D, STORE8, FP8>::THREADS), (TileSha
         return;
     }
     // Precision guard (e4m3 MFMAs): l / 2^6 is the row's probability mass
-    // sum_k 2^(x_k - m) against the running reference.
-    if (FP8 && a.guard_mass && row_ok && h == 0) a.guard_mass[row_index] = st.l * (1.f / 64.f);
+    // sum_k 2^(x_k - m) against the running reference; a row below its KV
+    // head's threshold joins the guard plan.
+    if (FP8 && a.guard_thr) {
+        const float thr = guard_threshold(a.guard_thr, head, D / 16);
+        if (row_ok && h == 0 && st.l * (1.f / 64.f) < thr)
+            guard_append(a.guard_rows, a.num_kv_heads, a.rows_per_head, head, er.row);
+    }
     float hist_weight = 0.f;
     if (CAUSAL && a.merge_o) {
         // out = (e^lse_h O_h + e^lse O) / (e^lse_h + e^lse)

@@ -161,7 +161,7 @@ def _softmax_walk(scores, v_tiles, tiles, cscale, kernel, exp2, q_round=True, p_
 
 
 GUARD_MIN_MASS = 384.0
-VSTATS_KEYS = 8192
+VSTATS_KEYS = 2048
 
 
 def guard_thresholds(pool_codes, block_table, page_valid_len, *, num_kv_heads, block_size, head_dim, v_scale=1.0):

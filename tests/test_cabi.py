@@ -129,11 +129,12 @@ def test_split_workspace_size_from_python():
                                                             kv_dtype="bfloat16"))
     assert bf16.split_workspace_bytes(3) == 3 * rows * (cfg.head_dim + 2) * 4
     assert kernel.workspace_bytes(1, precision="fp8") == 0
-    # the precision guard needs its row masses, plan and fixup partials even
-    # for one pass (a split call's merge takes the masses from the partials)
+    # the precision guard needs its thresholds, plan (row counts and a list
+    # slot per row) and fixup partials even for one pass, and the same
+    # beside a split call's partials
     guard = kernel.workspace_bytes(1, precision="auto")
-    assert guard >= 4 * rows + 4 * (4 + rows // 128)
-    assert kernel.workspace_bytes(3, precision="auto") >= kernel.split_workspace_bytes(3) + guard - 4 * rows
+    assert guard >= 4 * (4 + rows) + cfg.num_kv_heads * cfg.head_dim // 16 * 4
+    assert kernel.workspace_bytes(3, precision="auto") == kernel.split_workspace_bytes(3) + guard
     with pytest.raises(_native.PcpaError, match="BAD_SHAPE"):
         kernel.split_workspace_bytes(_native.MAX_SPLITS + 1)
 

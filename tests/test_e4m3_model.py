@@ -243,18 +243,18 @@ def test_guard_threshold_closed_forms():
 
 
 def test_guard_threshold_samples_every_s_th_key_of_long_walks():
-    """Beyond 8192 valid keys the statistics take every s-th key of each
+    """Beyond 2048 valid keys the statistics take every s-th key of each
     page (s a power of two): keys off the stride do not count."""
     cfg = PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=32768, actual_history_len=32768,
                              block_size=512, interleave_size=64, num_q_heads=4, num_kv_heads=1, head_dim=64,
                              backend="hip").validate()
     keys = np.arange(512)[:, None]
-    # on the stride (4: 32768 keys / 4 = 8192) alternate +-1; off it 448
-    v = np.where(keys % 4 == 0, np.where((keys // 4) % 2 == 0, 1.0, -1.0), 448.0)
+    # on the stride (16: 32768 keys / 16 = 2048) alternate +-1; off it 448
+    v = np.where(keys % 16 == 0, np.where((keys // 16) % 2 == 0, 1.0, -1.0), 448.0)
     pool = _pool_with_v(cfg, lambda page, h: np.broadcast_to(v, (512, 64)).astype(np.float32))
     kw = dict(num_kv_heads=1, block_size=512, head_dim=64)
     np.testing.assert_allclose(em.guard_thresholds(*pool, v_scale=1.0, **kw), [384.0], rtol=1e-12)
-    # half the history: 16384 keys, every other one (448 among them)
+    # half the history: 16384 keys, every eighth one (448 among them)
     lens = pool[2].copy()
     lens[:, cfg.max_local_blocks // 2:] = 0
     full = em.guard_thresholds(pool[0], pool[1], lens, v_scale=1.0, **kw)
