@@ -84,12 +84,13 @@ class HistoryAttentionKernel:
       MFMAs (Q and P rounded to e4m3), ``"bf16"`` as BF16 MFMAs on the exactly
       widened cache, and ``"auto"`` (default) runs e4m3 MFMAs with the
       precision guard: every row whose probability mass
-      ``sum_k 2^(x_k - m)`` is below ``_native.GUARD_MIN_MASS`` - few valid
-      keys, or a peaked score distribution, where the e4m3 rounding of Q and
-      P is not averaged away - is recomputed on the device with BF16 MFMAs
-      (a second launch whose workgroups exit at once when they hold no such
-      row).  The decision is made per row on the GPU from the runtime
-      lengths and data; nothing is read back to the host.
+      ``sum_k 2^(x_k - m)`` is below its KV head's threshold
+      ``_native.GUARD_MIN_MASS * v_scale^2 * max_d Var(V[h, :, d])`` - few
+      valid keys, a peaked score distribution or a wide V, where the e4m3
+      rounding of Q and P is not averaged away - is recomputed on the
+      device with BF16 MFMAs (a later launch whose workgroups exit at once
+      when they hold no such row).  The decision is made per row on the GPU
+      from the runtime lengths and data; nothing is read back to the host.
     * ``exp2``: how the e4m3 MFMA path at head_dim 256 forms the e4m3
       probabilities.  ``"fast"`` (default) writes the e4m3 code of 2^x
       directly, interpolating the exponential linearly between powers of two
@@ -463,7 +464,7 @@ class HistoryAttentionKernel:
 
         Calls on one stream run in order, so they can share one; calls on
         different streams may overlap on the GPU, so each stream gets its own
-        (a guarded call's row flags, plan and fixup partials, or a split
+        (a guarded call's thresholds, plan and fixup partials, or a split
         call's partials, must not be rewritten by another call in flight).
         """
         import torch

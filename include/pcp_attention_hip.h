@@ -72,17 +72,21 @@ extern "C" {
  * runs e4m3 MFMAs (an e4m3 cache without PCPA_FLAG_BF16_MFMA); this bit
  * asks for it explicitly and changes nothing else.
  * e4m3 Q and P carry ~3.6% relative rounding noise per element, which
- * averages away only when many keys share a row's softmax.  The e4m3 pass
- * therefore also measures each row's probability mass
+ * averages away only when many keys share a row's softmax, and the error
+ * grows with the spread of V.  A first launch measures, per KV head h, the
+ * threshold
+ *     thr_h = PCPA_GUARD_MIN_MASS * v_scale^2 * max_d Var_k(V[h, k, d])
+ * (the variance per channel of the e4m3 V codes over up to 2048 sampled
+ * keys of the walk); the e4m3 pass measures each row's probability mass
  *     W = sum_k 2^(x_k - m)        (x_k the score in log2 units, m the
  *                                    running reference, at most 2.5 below
  *                                    the row's largest x_k)
  * and a later launch recomputes, with BF16 MFMAs on the exactly widened
- * cache (bf16 Q and P), every row with W < PCPA_GUARD_MIN_MASS (short
- * histories and peaked score distributions), the rows gathered 128 to a
- * workgroup.  Its workgroups exit at once when no row is listed.  Its
- * buffers (row flags, per-head row lists, the recomputation's partials)
- * are in the caller's workspace (pcpa_history_attention_split, sized by
+ * cache (bf16 Q and P), every row with W < thr_h (short histories, peaked
+ * score distributions, wide V), the rows gathered 128 to a workgroup.  Its
+ * workgroups exit at once when no row is listed.  Its buffers (thresholds,
+ * per-head row lists, the recomputation's partials) are in the caller's
+ * workspace (pcpa_history_attention_split, sized by
  * pcpa_split_workspace_bytes), the allocation-free array
  * (pcpa_history_attention_noalloc) or, for pcpa_history_attention / _lse,
  * the library's guard scratch; a launch whose guard buffers exceed
