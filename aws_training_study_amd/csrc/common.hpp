@@ -237,12 +237,17 @@ __host__ __device__ __forceinline__ constexpr int lds_row(int key) {
 // transposing V reads bank-conflict free (measured with the LDS
 // bank-conflict counter on gfx950, per read pattern).  BF16 rows of 128
 // bytes (head_dim 64) sit in alternate halves of the 64 banks, so their K
-// swizzle spreads even and odd rows over all 8 chunks each.
+// swizzle spreads even and odd rows over all 8 chunks each.  BF16 rows of
+// 512 bytes (head_dim 256) swap the two bit pairs of the row: a bijection
+// on the 16 rows a 16-lane score read covers, and distinct in chunk bits
+// 2-3 over every 4-row block a 32-lane transposing V read covers, so K and
+// V share one swizzle (and one set of lane DMA offsets) with no conflicts.
 template <bool FP8, int CHUNKS>
 __device__ __forceinline__ int chunk_swizzle(int row) {
     constexpr int mask = (CHUNKS < 16 ? CHUNKS : 16) - 1;
     if constexpr (FP8) return row & 15 & mask;
     if constexpr (CHUNKS == 8) return (row >> 1) & 7;
+    if constexpr (CHUNKS == 32) return ((row & 3) << 2) | ((row >> 2) & 3);
     return (((row & 7) << 1) | ((row >> 3) & 1)) & mask;
 }
 // FP8 V tiles use an even-only swizzle: the two 16-lane groups of a
@@ -253,14 +258,14 @@ __device__ __forceinline__ int chunk_swizzle(int row) {
 // 4s + 3) would share their chunk block under the score swizzle (2-way
 // conflicts, 1.8 extra cycles per read); flipping chunk bit 3 on odd rows
 // separates them (GQA-8 workload 1.99 -> 1.97 ms).  Other BF16 rows keep
-// the score operand's former swizzle: 128-byte rows are conflict-free with
-// it, and for 512-byte rows (head_dim 256, key-split pairs) the flip
-// measured slower (the extra lane-address work costs more than the
-// conflicts, which the partner wave hides).
+// the score operand's swizzle: 128-byte rows are conflict-free with it,
+// and 512-byte rows have one made for both reads (a flip for V alone
+// measured slower there: separate V DMA offsets cost lane-address work).
 template <bool FP8, int CHUNKS>
 __device__ __forceinline__ int chunk_swizzle_v(int row) {
     constexpr int mask = (CHUNKS < 16 ? CHUNKS : 16) - 1;
     if constexpr (FP8) return (2 * row) & mask & 14;
+    if constexpr (CHUNKS == 32) return chunk_swizzle<false, CHUNKS>(row);
     const int s = (((row & 7) << 1) | ((row >> 3) & 1)) & mask;
     if constexpr (CHUNKS == 16) return s ^ ((row & 1) << 3);
     return s;
