@@ -249,6 +249,42 @@ def test_auto_meets_the_bar_with_wide_v(bucket, cuda_device):
     _check_bar(_pick(auto, sample), ref, f"{label} auto")
 
 
+@pytest.mark.parametrize("q_factor", [1.5, 2.0])
+def test_guard_on_a_table_of_two_staging_chunks(q_factor, cuda_device):
+    """2048 table entries (64 ranks x 32 pages of 64 tokens, 131072 keys):
+    the V statistics stage the table in two chunks of 1024 entries.  V ~
+    N(0, 4) (threshold ~4 x 384); Q x1.5 puts ~2% of the rows below it (a
+    sparse fixup over ~20 groups, ~11 ranges each), Q x2 most (dense).
+    Sampled rows above 1.25x the model's threshold keep the e4m3 pass's
+    output bit for bit, rows below 0.8x get the BF16-MFMA result (to the
+    rounding of the fixup's ranges), and the default call meets the bar."""
+    cfg = replace(FULL, block_size=64).validate()
+    assert cfg.pcp_size * cfg.max_local_blocks > 1024
+    problem = _problem(cfg, "none", 49, 2.0)
+    q = _scaled_q(problem, q_factor)
+    print(f"case 2048 entries of 64 tokens, V x2, Q x{q_factor}", flush=True)
+    gpu = problem.to(cuda_device)
+    qd = q.to(cuda_device)
+    kernel = make_history_attention_kernel(cfg)
+    kw = dict(page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale, v_scale=problem.v_scale)
+    auto = kernel(qd, gpu.kv_pages, gpu.block_table, **kw)
+    fp8 = kernel(qd, gpu.kv_pages, gpu.block_table, precision="fp8", splits=1, **kw)
+    bf16 = kernel(qd, gpu.kv_pages, gpu.block_table, precision="bf16", splits=1, **kw)
+    torch.cuda.synchronize()
+    rows = _sample(cfg, 94, 49)
+    _, _, mass = _model(problem, q, rows, problem.page_valid_len, return_mass=True)
+    thr = _thresholds(problem, problem.page_valid_len, rows)
+    kept, low = mass > 1.25 * thr, mass < 0.8 * thr
+    print(f"thresholds {np.round(np.unique(thr), 1)}; rows kept {kept.sum()}, recomputed {low.sum()} of "
+          f"{len(rows)}", flush=True)
+    assert 3 * 384 < thr.min() and thr.max() < 5 * 384
+    assert kept.sum() > 0 and low.sum() > 0
+    a, f, b = _pick(auto, rows), _pick(fp8, rows), _pick(bf16, rows)
+    assert np.array_equal(a[kept], f[kept])
+    assert np.abs(a[low] - b[low]).max() <= 4e-3
+    _check_bar(a, _paged_reference(problem, q, rows, problem.page_valid_len), f"2048 entries Q x{q_factor} auto")
+
+
 # ---- the e4m3 log-sum-exp (the prefill merge's weights)
 
 
