@@ -55,23 +55,39 @@ struct WriteArgs {
     int32_t num_pages;
     int32_t head_dim;
     float k_scale, v_scale;
+    float k_rcp, v_rcp;  // RN(1 / scale), for div_rn when fast_div
+    int32_t fast_div;    // both scales in [2^-80, 2^126]: div_rn instead of the IEEE division
 };
 
-// e4m3 code of x (round to nearest even; magnitudes above 464 and infinities
-// become the NaN code 0x7f with x's sign, like torch's float8_e4m3fn cast;
-// v_cvt_pk_fp8_f32 agrees except that it writes 0xff for every NaN input).
+// x / d rounded to nearest even, as the IEEE division rounds it, from y =
+// RN(1 / d) by Markstein's correction (P. Markstein, IBM J. Res. Develop.
+// 34(1), 1990, 111-119): q0 = RN(x y) is within an ulp of
+// x / d, the remainder x - d q0 is exact (one FMA), and RN(q0 + r y) is
+// RN(x / d).  Three instructions and a sign copy where the IEEE sequence
+// takes ten.  Compared with exact quotients for bf16 x with |x| and
+// |x / d| >= 2^-100 and d from 2^-80 to 2^126; below that the quotient
+// rounds to an e4m3 zero either way, and zeros, infinities, NaNs and
+// overflowing quotients give a NaN or a signed zero here where the IEEE
+// quotient is an infinity, a NaN or a signed zero: the same e4m3 code (the
+// NaN code or zero with x's sign, which copysign keeps).
+__device__ __forceinline__ float div_rn(float x, float d, float y) {
+    const float q0 = x * y;
+    const float r = fmaf(-d, q0, x);
+    return copysignf(fmaf(r, y, q0), x);
+}
+
+// e4m3 codes of four values (round to nearest even; magnitudes above 464
+// and infinities become the NaN code 0x7f with the value's sign, like
+// torch's float8_e4m3fn cast).  v_cvt_pk_fp8_f32 gives these codes except
+// that it writes 0xff for every NaN; every other code's sign bit is already
+// the value's, so each code's bit 7 is set from its value's sign bit (byte 3
+// of the float, gathered by two byte permutes).
 __device__ __forceinline__ uint32_t e4m3_codes4(float a, float b, float c, float d) {
     int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
     w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
-    uint32_t u = (uint32_t)w;
-    const float x[4] = {a, b, c, d};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if (__builtin_isnan(x[i])) {
-            const uint32_t code = (__float_as_uint(x[i]) >> 31) ? 0xffu : 0x7fu;
-            u = (u & ~(0xffu << (8 * i))) | (code << (8 * i));
-        }
-    return u;
+    const uint32_t lo = __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x0c0c0703u);
+    const uint32_t hi = __builtin_amdgcn_perm(__float_as_uint(d), __float_as_uint(c), 0x07030c0cu);
+    return ((uint32_t)w & 0x7f7f7f7fu) | ((lo | hi) & 0x80808080u);
 }
 
 // One thread per (token, 8-element chunk) of head blockIdx.y: the token's
@@ -124,11 +140,24 @@ __global__ void __launch_bounds__(kThreads) kv_write_kernel(WriteArgs a, uint32_
         float kf[8], vf[8];
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            // x / scale with IEEE division, as torch computes (x / scale).to(float8)
-            kf[2 * w] = bf16_bits_to_f32((uint32_t)kin[w] & 0xffffu) / a.k_scale;
-            kf[2 * w + 1] = bf16_bits_to_f32((uint32_t)kin[w] >> 16) / a.k_scale;
-            vf[2 * w] = bf16_bits_to_f32((uint32_t)vin[w] & 0xffffu) / a.v_scale;
-            vf[2 * w + 1] = bf16_bits_to_f32((uint32_t)vin[w] >> 16) / a.v_scale;
+            kf[2 * w] = bf16_bits_to_f32((uint32_t)kin[w] & 0xffffu);
+            kf[2 * w + 1] = bf16_bits_to_f32((uint32_t)kin[w] >> 16);
+            vf[2 * w] = bf16_bits_to_f32((uint32_t)vin[w] & 0xffffu);
+            vf[2 * w + 1] = bf16_bits_to_f32((uint32_t)vin[w] >> 16);
+        }
+        // x / scale rounded as torch's (x / scale).to(float8) rounds it
+        if (a.fast_div) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                kf[i] = div_rn(kf[i], a.k_scale, a.k_rcp);
+                vf[i] = div_rn(vf[i], a.v_scale, a.v_rcp);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                kf[i] = kf[i] / a.k_scale;
+                vf[i] = vf[i] / a.v_scale;
+            }
         }
         *(v2i*)dst = v2i{(int)e4m3_codes4(kf[0], kf[1], kf[2], kf[3]), (int)e4m3_codes4(kf[4], kf[5], kf[6], kf[7])};
         *(v2i*)(dst + a.v_offset) =

@@ -631,6 +631,10 @@ int32_t pcpa_kv_cache_write(const pcpa_params* p, int32_t interleave, int64_t fi
     a.head_dim = p->head_dim;
     a.k_scale = p->k_scale;
     a.v_scale = p->v_scale;
+    a.k_rcp = 1.f / p->k_scale;
+    a.v_rcp = 1.f / p->v_scale;
+    auto div_ok = [](float d) { return d >= 0x1p-80f && d <= 0x1p126f; };
+    a.fast_div = div_ok(p->k_scale) && div_ok(p->v_scale) ? 1 : 0;
     const uint32_t row_chunks = (uint32_t)num_tokens * (uint32_t)(p->head_dim / 8);
     const dim3 grid((row_chunks + pcpa::cache::kThreads - 1) / pcpa::cache::kThreads, p->num_kv_heads);
     const dim3 block(pcpa::cache::kThreads);

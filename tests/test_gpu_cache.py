@@ -115,7 +115,11 @@ def test_absmax_propagates_nan_like_torch(cuda_device):
 
 def test_e4m3_codes_match_torch_cast(cuda_device):
     """Round-to-nearest-even, the 448/464/480 boundary, subnormals, signed zeros,
-    infinities and NaN: the producer's codes equal torch's float8_e4m3fn cast."""
+    infinities and NaN: the producer's codes equal torch's float8_e4m3fn cast,
+    for scales on both sides of the reciprocal-based division's range [2^-80,
+    2^126] (inside it the quotient is RN(x * RN(1/d)) corrected by one FMA
+    remainder step; outside it the IEEE division), over finite bf16 values of
+    every exponent."""
     cfg = PCPAttentionConfig(pcp_size=1, num_q_heads=2, num_kv_heads=1, head_dim=64, current_len=64,
                              max_history_len=64, actual_history_len=64, block_size=64, interleave_size=64,
                              kv_dtype="fp8_e4m3fn", backend="hip").validate()
@@ -126,10 +130,15 @@ def test_e4m3_codes_match_torch_cast(cuda_device):
     gen = torch.Generator().manual_seed(3)
     sweep = torch.randn(64 * 64 - special.numel(), generator=gen) * torch.exp2(torch.randint(-12, 10, (64 * 64 - special.numel(),),
                                                                                                generator=gen).float())
-    x = torch.cat([special, sweep]).to(torch.bfloat16).reshape(1, 64, 64)
+    sweep = sweep[:2048]
+    n_bits = 64 * 64 - special.numel() - sweep.numel()
+    bits = torch.randint(0, 0x7F80, (n_bits,), generator=gen, dtype=torch.int32)
+    bits |= torch.randint(0, 2, (n_bits,), generator=gen, dtype=torch.int32) << 15
+    every_exponent = bits.to(torch.int16).view(torch.bfloat16).float()
+    x = torch.cat([special, sweep, every_exponent]).to(torch.bfloat16).reshape(1, 64, 64)
     pool = torch.zeros((cfg.num_pages, cfg.page_elements), dtype=torch.float8_e4m3fn, device=cuda_device)
     table = torch.arange(cfg.num_pages, dtype=torch.int32).reshape(1, -1).to(cuda_device)
-    for scale in (1.0, 0.37):
+    for scale in (1.0, 0.37, 2.0 ** -80, 0.75 * 2.0 ** -80, 3e-30, 1e30, 2.0 ** 126, 1.5 * 2.0 ** 126, 1e-40):
         KVCacheWriter(cfg)(x.to(cuda_device), x.to(cuda_device), pool, table, k_scale=scale, v_scale=scale)
         torch.cuda.synchronize()
         expect = (x.float() / scale).to(torch.float8_e4m3fn).view(torch.uint8).reshape(-1)
