@@ -324,9 +324,9 @@ __global__ void __launch_bounds__(kVStatsThreads) guard_vstats_kernel(VStatsArgs
     const int b = tid >> 4, p = tid & 15;
     int64_t t1 = 0, t2 = 0;
 #pragma unroll
-    for (int i = p; i < T; i += 16) {
-        t1 += s1[b][i];
-        t2 += s2[b][i];
+    for (int k = 0; k < T / 16; ++k) {
+        t1 += s1[b][p + 16 * k];
+        t2 += s2[b][p + 16 * k];
     }
 #pragma unroll
     for (int off = 1; off < 16; off <<= 1) {
