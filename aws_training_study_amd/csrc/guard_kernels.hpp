@@ -41,17 +41,20 @@ constexpr int64_t kGuardPartialRows = 32768;
 // rows in slot order, guard_ranges()) merged by log-sum-exp (as
 // merge_splits_kernel) into out (bf16) and lse; workgroup b takes slot rows
 // b, b + gridDim.x, ... .  Thread t takes 8 consecutive d (t % d_vec8) of
-// the ranges t / d_vec8, t / d_vec8 + groups, ...; the groups' sums meet in
-// LDS, so the dependent loads per thread are ranges / groups rather than
-// ranges.  Dense mode: nothing.
+// the ranges t / d_vec8, t / d_vec8 + groups, ... (at most kGuardMergePer:
+// the host caps ranges at 64, and groups >= 8), loads all their log-sum-exps and partials
+// at once and sums them against its own largest log-sum-exp; the groups'
+// sums meet in LDS, rescaled to the row's largest.  Dense mode: nothing.
 constexpr int kGuardMergeThreads = 256;
 constexpr int kGuardMergeGroups = 512;  // workgroups of guard_merge_kernel
+constexpr int kGuardMergePer = 8;       // ranges per thread at most
 
 __global__ void __launch_bounds__(kGuardMergeThreads) guard_merge_kernel(const float* part_o, const float* part_lse,
                                                                          const int32_t* plan, GuardShape g,
                                                                          int d_vec8, uint8_t* out, float* lse_out) {
     __shared__ float red[kGuardMergeThreads * 8];
     __shared__ float wred[kGuardMergeThreads];
+    __shared__ float mred[kGuardMergeThreads];
     const int listed = guard_groups(plan, g.num_kv_heads);
     const int ranges = guard_ranges(listed, g.partial_rows, g.max_ranges);
     if (ranges == 0) return;
@@ -66,48 +69,66 @@ __global__ void __launch_bounds__(kGuardMergeThreads) guard_merge_kernel(const f
         const GuardGroup gg = guard_group(plan, g.num_kv_heads, slot);
         const int idx = gg.first + (int)(slot_row - (int64_t)slot * kRowsPerGroup);
         if (idx >= gg.count) continue;  // the same for the whole workgroup
+        float lk[kGuardMergePer];
+        v4f lo[kGuardMergePer], hi[kGuardMergePer];
+#pragma unroll
+        for (int k = 0; k < kGuardMergePer; ++k) {
+            const int sp = sg + k * groups;
+            lk[k] = -INFINITY;
+            lo[k] = hi[k] = v4f{0.f, 0.f, 0.f, 0.f};
+            if (sp < ranges) {
+                lk[k] = part_lse[sp * stride + slot_row];
+                const float* const src = part_o + (sp * stride + slot_row) * D + d0;
+                lo[k] = *(const v4f*)src;
+                hi[k] = *(const v4f*)(src + 4);
+            }
+        }
         const int r = plan[guard_list_offset(g.num_kv_heads) + gg.head * guard_head_segment(g.rows_per_head) + idx];
         const int64_t row = guard_row_index(g, gg.head, r);
-        // every thread finds the largest range lse (few loads, all in flight)
         float mx = -INFINITY;
-#pragma unroll 8
-        for (int sp = 0; sp < ranges; ++sp) mx = fmaxf(mx, part_lse[sp * stride + slot_row]);
+#pragma unroll
+        for (int k = 0; k < kGuardMergePer; ++k) mx = fmaxf(mx, lk[k]);
         float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         float wsum = 0.f;
-#pragma unroll 8
-        for (int sp = sg; sp < ranges; sp += groups) {
-            const float l = part_lse[sp * stride + slot_row];
-            const float w = l == -INFINITY ? 0.f : __expf(l - mx);
+#pragma unroll
+        for (int k = 0; k < kGuardMergePer; ++k) {
+            const float w = lk[k] == -INFINITY ? 0.f : __expf(lk[k] - mx);
             wsum += w;
-            const float* const src = part_o + (sp * stride + slot_row) * D + d0;
-            const v4f lo = *(const v4f*)src, hi = *(const v4f*)(src + 4);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                acc[i] = fmaf(w, lo[i], acc[i]);
-                acc[4 + i] = fmaf(w, hi[i], acc[4 + i]);
+                acc[i] = fmaf(w, lo[k][i], acc[i]);
+                acc[4 + i] = fmaf(w, hi[k][i], acc[4 + i]);
             }
         }
         __syncthreads();  // the previous row's sums are read
 #pragma unroll
         for (int i = 0; i < 8; ++i) red[tid * 8 + i] = acc[i];
         wred[tid] = wsum;
+        mred[tid] = mx;
         __syncthreads();
         if (sg == 0) {
-            for (int o = 1; o < groups; ++o) {
+            float m = mx;
+            for (int o = 1; o < groups; ++o) m = fmaxf(m, mred[o * d_vec8 + tid]);
+            float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            float ws = 0.f;
+            for (int o = 0; o < groups; ++o) {
                 const int t = o * d_vec8 + tid;
+                const float mo = mred[t];
+                if (mo == -INFINITY) continue;  // no range of this group has valid keys
+                const float f = __expf(mo - m);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc[i] += red[t * 8 + i];
-                wsum += wred[t];
+                for (int i = 0; i < 8; ++i) sum[i] = fmaf(f, red[t * 8 + i], sum[i]);
+                ws = fmaf(f, wred[t], ws);
             }
-            const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+            const float inv = ws > 0.f ? 1.f / ws : 0.f;
             uint32_t wv[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const __bf16 x0 = (__bf16)(acc[2 * i] * inv), x1 = (__bf16)(acc[2 * i + 1] * inv);
+                const __bf16 x0 = (__bf16)(sum[2 * i] * inv), x1 = (__bf16)(sum[2 * i + 1] * inv);
                 wv[i] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
             }
             *(v4i*)(out + (row * D + d0) * 2) = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
-            if (lse_out && d0 == 0) lse_out[row] = wsum > 0.f ? mx + __logf(wsum) : -INFINITY;
+            if (lse_out && d0 == 0) lse_out[row] = ws > 0.f ? m + __logf(ws) : -INFINITY;
         }
     }
 }

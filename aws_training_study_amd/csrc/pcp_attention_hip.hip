@@ -114,8 +114,11 @@ inline WorkspaceLayout workspace_layout(const pcpa_params* p, int splits) {
         const int64_t key_tiles = entries * (p->block_size / kKeyTile);
         const int64_t rows_per_head = rows / p->num_q_heads * (p->num_q_heads / p->num_kv_heads);
         w.groups_total = (int32_t)((rows_per_head + kRowsPerGroup - 1) / kRowsPerGroup * p->num_kv_heads);
+        constexpr int64_t kMaxRanges = 64;
+        static_assert(kMaxRanges <= kGuardMergePer * (kGuardMergeThreads / (256 / 8)),
+                      "guard_merge_kernel's threads hold every range at head_dim 256");
         int64_t mr = key_tiles / 2;
-        mr = mr < 1 ? 1 : mr > 64 ? 64 : mr;
+        mr = mr < 1 ? 1 : mr > kMaxRanges ? kMaxRanges : mr;
         w.max_ranges = (int32_t)mr;
         int64_t prows = mr >= 2 ? (int64_t)w.groups_total * kRowsPerGroup * mr : 0;
         prows = prows < kGuardPartialRows ? prows : kGuardPartialRows;
