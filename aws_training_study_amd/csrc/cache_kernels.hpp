@@ -159,12 +159,18 @@ __global__ void __launch_bounds__(kThreads) kv_write_kernel(WriteArgs a, uint32_
                 vf[i] = vf[i] / a.v_scale;
             }
         }
-        *(v2i*)dst = v2i{(int)e4m3_codes4(kf[0], kf[1], kf[2], kf[3]), (int)e4m3_codes4(kf[4], kf[5], kf[6], kf[7])};
-        *(v2i*)(dst + a.v_offset) =
-            v2i{(int)e4m3_codes4(vf[0], vf[1], vf[2], vf[3]), (int)e4m3_codes4(vf[4], vf[5], vf[6], vf[7])};
+        // streaming (non-temporal) stores: the pool is written once and read
+        // by later launches, so its lines need not stay in this launch's L2
+        // (full-fp8 history: 73 -> 59 us with the division above)
+        __builtin_nontemporal_store(
+            v2i{(int)e4m3_codes4(kf[0], kf[1], kf[2], kf[3]), (int)e4m3_codes4(kf[4], kf[5], kf[6], kf[7])},
+            (v2i*)dst);
+        __builtin_nontemporal_store(
+            v2i{(int)e4m3_codes4(vf[0], vf[1], vf[2], vf[3]), (int)e4m3_codes4(vf[4], vf[5], vf[6], vf[7])},
+            (v2i*)(dst + a.v_offset));
     } else {
-        *(v4i*)dst = kin;
-        *(v4i*)(dst + a.v_offset) = vin;
+        __builtin_nontemporal_store(kin, (v4i*)dst);
+        __builtin_nontemporal_store(vin, (v4i*)(dst + a.v_offset));
     }
 }
 
