@@ -296,7 +296,8 @@ inline int32_t history_launch(const pcpa_params* p, int splits, const void* q, c
         const int d_vec8 = p->head_dim / 8;
         const int64_t threads = g.rows_total * d_vec8;
         auto merge = splits == 2 ? merge_splits_kernel<2> : splits == 3 ? merge_splits_kernel<3>
-                   : splits == 4 ? merge_splits_kernel<4> : merge_splits_kernel<0>;
+                   : splits == 4 ? merge_splits_kernel<4> : splits == 8 ? merge_splits_kernel<8>
+                   : merge_splits_kernel<0>;
         hipLaunchKernelGGL(merge, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
                            (const float*)a.part_o, a.part_f16, a.part_f16 ? p->v_scale : 1.f,
                            (const float*)a.part_lse, splits, g.rows_total, d_vec8,
