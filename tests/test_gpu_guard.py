@@ -355,6 +355,41 @@ def test_tile_kernel_e4m3_matches_model(head_dim, tokens, cuda_device):
                f"tile D={head_dim} L={tokens} auto")
 
 
+@pytest.mark.parametrize("splits", [1, 2])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_tile_kernel_guard_recomputes_the_low_mass_rows(head_dim, splits, cuda_device):
+    """The tile kernel's e4m3 path on an 8K history: about a fifth of the rows
+    fall below their KV head's threshold.  Rows whose model mass is above
+    1.25x it keep the e4m3 pass's output bit for bit; rows below 0.8x get the
+    BF16-MFMA result, to the rounding of the fixup's walk split into ranges
+    and merged by guard_merge_kernel (whose lanes take the ranges in 32 or 16
+    groups at head_dim 64 or 128).  splits 2: the split merge lists the rows."""
+    cfg = PCPAttentionConfig(pcp_size=4, current_len=256, max_history_len=8192, actual_history_len=8192,
+                             block_size=256, interleave_size=64, num_q_heads=16, num_kv_heads=2, head_dim=head_dim,
+                             backend="hip").validate()
+    problem = _problem(cfg, "none", 47)
+    print(f"case tile guard D={head_dim} splits {splits}", flush=True)
+    gpu = problem.to(cuda_device)
+    kernel = make_history_attention_kernel(cfg)
+    kw = dict(page_valid_len=gpu.page_valid_len, k_scale=problem.k_scale, v_scale=problem.v_scale)
+    q = gpu.q_stacked
+    auto = kernel(q, gpu.kv_pages, gpu.block_table, splits=splits, **kw).float().cpu().numpy()
+    fp8 = kernel(q, gpu.kv_pages, gpu.block_table, precision="fp8", splits=splits, **kw).float().cpu().numpy()
+    bf16 = kernel(q, gpu.kv_pages, gpu.block_table, precision="bf16", splits=1, **kw).float().cpu().numpy()
+    torch.cuda.synchronize()
+    _, _, mass = _model(problem, problem.q_stacked, None, problem.page_valid_len, kernel="tile", exp2="exact",
+                        splits=splits, return_mass=True)
+    thr = _thresholds(problem, problem.page_valid_len)
+    group = cfg.num_q_heads // cfg.num_kv_heads
+    T = np.repeat(thr, group)[None, :, None]
+    kept, low = mass > 1.25 * T, mass < 0.8 * T
+    print(f"rows kept {kept.sum()}, recomputed {low.sum()} of {mass.size}", flush=True)
+    assert kept.sum() > 0 and low.sum() > 0
+    assert np.array_equal(auto[kept], fp8[kept])
+    assert np.abs(auto[low] - bf16[low]).max() <= 2e-3
+    assert np.abs(auto[low] - fp8[low]).max() > 0
+
+
 # ---- what the guard recomputes
 
 
